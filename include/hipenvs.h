@@ -1,0 +1,91 @@
+/*
+ * hipenvs: the C ABI of the MI355X (gfx950) batched-environment library.
+ *
+ * Every entry point enqueues its kernel(s) on `stream` and returns without
+ * synchronising; the caller owns the device boundary. The caller allocates
+ * every buffer (device memory, fp32 structure-of-arrays state of shape
+ * (rows, n), row-major, contiguous); the library allocates nothing, frees
+ * nothing and keeps no per-call state, so any host thread may call it on any
+ * stream. Inputs are never written.
+ *
+ * Return value: HIPENVS_OK (0), or a negative HIPENVS_E_* code. On
+ * HIPENVS_E_HIP the launch failed and hipenvs_last_hip_error() gives the
+ * hipError_t of the calling thread's most recent failure.
+ *
+ * RNG: `seed` is the per-call counter of the reference's step modules
+ * (cartpole_metal.py:106-117 pre-increments it before each launch). Reset
+ * noise for env i at counter s is pcg_hash((s ^ (i * 0x9E3779B9)) + row
+ * offset), uniform from the top 24 bits (cartpole_metal.py:39-51,89-93).
+ *
+ * Each declaration names the reference interface it replaces (file:line in
+ * metal-rl-envs).
+ */
+#ifndef HIPENVS_H
+#define HIPENVS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipenvs_stream_t; /* a hipStream_t; NULL = the null stream */
+
+enum {
+  HIPENVS_OK = 0,
+  HIPENVS_E_ARG = -1,         /* null pointer with n > 0, negative size, bad parameter */
+  HIPENVS_E_UNSUPPORTED = -2, /* a compile-time shape (hidden, K links, C legs) with no instantiation */
+  HIPENVS_E_HIP = -3          /* the HIP launch failed; see hipenvs_last_hip_error() */
+};
+
+/* Library version and build description, e.g. "hipenvs 0.1 gfx950 fp-contract=off". */
+const char* hipenvs_version(void);
+
+/* hipError_t (as int) of this thread's last failed launch; 0 if none. */
+int hipenvs_last_hip_error(void);
+
+/* ---- CartPole ---------------------------------------------------------- */
+
+/* Fresh states (4, n): what a reset column gets at counter `seed`.
+ * Replaces cartpole_mlx.reset (cartpole_mlx.py:30-31), re-exported by
+ * cartpole_metal.py:20; uses the kernel's counter RNG instead of MLX's. */
+int hipenvs_cartpole_reset(float* state, int64_t n, uint32_t seed, hipenvs_stream_t stream);
+
+/* One Gym CartPole step for n envs with masked auto-reset.
+ * state (4, n) f32, action (n) i32 (1 pushes right, anything else left)
+ * -> next_state (4, n) f32, reward (n) f32 (= 1), done (n) u8 (0/1).
+ * Replaces the `cartpole_step` Metal kernel and cartpole_metal.step
+ * (cartpole_metal.py:69-125). */
+int hipenvs_cartpole_step(const float* state, const int32_t* action, uint32_t seed,
+                          float* next_state, float* reward, uint8_t* done,
+                          int64_t n, hipenvs_stream_t stream);
+
+/* k chained CartPole steps in one launch, state kept in registers. Step t
+ * (0-based) uses counter seed + t and action actions[t * n + i], or, when
+ * `actions` is NULL, the in-kernel Bernoulli(0.5) action
+ * pcg_hash((seed + t) ^ (i * 0x9E3779B9) + 0x165667B1) >> 31.
+ * rewards and dones are (k, n). Identical to k calls of hipenvs_cartpole_step.
+ * No reference kernel: the semantic reference is a chain of k cartpole_metal.step
+ * calls evaluated once (bench.py:48-61, bench_kernel.py:14-22). */
+int hipenvs_cartpole_step_k(const float* state, const int32_t* actions, uint32_t seed, int32_t k,
+                            float* next_state, float* rewards, uint8_t* dones,
+                            int64_t n, hipenvs_stream_t stream);
+
+/* Bernoulli(0.5) (m == 2) or uniform [0, m) actions (m <= 256) for counter `seed`:
+ * bit 31, or ((h >> 8) * m) >> 24, of pcg_hash((seed ^ (i * 0x9E3779B9)) + 0x165667B1).
+ * The device-side action sampler of the benchmark loop (bench.py:55 samples
+ * mx.random.randint inside the loop). */
+int hipenvs_sample_actions(int32_t* action, int64_t n, int32_t m, uint32_t seed, hipenvs_stream_t stream);
+
+/* ---- Diagnostics (no reference counterpart) ---------------------------- */
+
+/* Elementwise deterministic sin, cos, tanh of x (n) as the kernels compute them;
+ * used by the parity tests to check the device transcendentals bit for bit. */
+int hipenvs_detmath(const float* x, float* sin_out, float* cos_out, float* tanh_out,
+                    int64_t n, hipenvs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIPENVS_H */

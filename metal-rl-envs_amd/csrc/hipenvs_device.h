@@ -1,0 +1,168 @@
+// Device-side building blocks shared by every hipenvs kernel: the counter RNG,
+// deterministic float32 transcendentals, launch geometry and the C-ABI error
+// plumbing. Compiled for gfx950 with -ffp-contract=off: every a*b+c below is a
+// rounded multiply followed by a rounded add, exactly as numpy evaluates it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hipenvs.h"
+
+namespace hipenvs {
+
+// ---------------------------------------------------------------------------
+// Counter RNG: the PCG hash of Jarzynski & Olano (JCGT 2020), the generator of
+// the reference's Metal kernels (cartpole_metal.py:39-51). Per-env stream
+// base seed ^ (env * 0x9E3779B9) (cartpole_metal.py:89).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kGolden = 0x9E3779B9u;
+constexpr uint32_t kRowStride = 0x85EBCA6Bu;        // generic row offset (pendulum_aba_metal.py:111)
+constexpr uint32_t kRowOff1 = 0x85EBCA6Bu;          // 4-row bodies (cartpole_metal.py:91-93)
+constexpr uint32_t kRowOff2 = 0xC2B2AE35u;
+constexpr uint32_t kRowOff3 = 0x27D4EB2Fu;
+constexpr uint32_t kActionOffset = 0x165667B1u;     // in-kernel actions (no reference counterpart)
+constexpr uint32_t kTorqueOffset = 0xD3A2646Cu;     // continuous torques (no reference counterpart)
+
+__device__ __forceinline__ uint32_t pcg_hash(uint32_t v) {
+  uint32_t s = v * 747796405u + 2891336453u;
+  uint32_t w = ((s >> ((s >> 28u) + 4u)) ^ s) * 277803737u;
+  return (w >> 22u) ^ w;
+}
+
+// float in [-bound, bound) from the top 24 bits of a hash (cartpole_metal.py:47-50).
+__device__ __forceinline__ float uniform_pm(uint32_t h, float bound) {
+  return ((float)(h >> 8) * (1.0f / 16777216.0f) * 2.0f - 1.0f) * bound;
+}
+
+__device__ __forceinline__ uint32_t env_hash(uint32_t seed, uint32_t env) { return seed ^ (env * kGolden); }
+
+__device__ __forceinline__ int32_t action_bit(uint32_t h) { return (int32_t)(pcg_hash(h + kActionOffset) >> 31); }
+
+__device__ __forceinline__ int32_t action_uniform(uint32_t h, uint32_t m) {
+  return (int32_t)(((pcg_hash(h + kActionOffset) >> 8) * m) >> 24);
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic float32 sin/cos/tanh. Built from IEEE operations only (no FMA,
+// no hardware transcendental), so numpy reproduces every bit; the numpy twin
+// and the derivation of every constant live with the CPU oracle. Accuracy vs
+// float64: <= 1.5 ULP (sin, cos), <= 2.5 ULP (tanh).
+// ---------------------------------------------------------------------------
+namespace dm {
+// pi/2 in four pieces of 12, 12, 12 and 24 significant bits: k*P1..k*P3 exact for |k| < 2^12.
+constexpr float PIO2_1 = 0x1.92p+0f;
+constexpr float PIO2_2 = 0x1.fb4p-12f;
+constexpr float PIO2_3 = 0x1.444p-24f;
+constexpr float PIO2_4 = 0x1.68c234p-39f;
+constexpr float TWO_OVER_PI = 0x1.45f306p-1f;
+// float64 fallback for |x| > 256: 33-bit head (exact products for |k| < 2^20) and tail.
+constexpr double PIO2_1D = 0x1.921fb544p+0;
+constexpr double PIO2_2D = 0x1.0b4611a626331p-34;
+constexpr double TWO_OVER_PI_D = 0x1.45f306dc9c883p-1;
+constexpr float SMALL_ARG = 256.0f;
+// Taylor coefficients 1/n! rounded to float32.
+constexpr float S3 = -0x1.555556p-3f, S5 = 0x1.111112p-7f, S7 = -0x1.a01a02p-13f, S9 = 0x1.71de3ap-19f;
+constexpr float C2 = -0x1p-1f, C4 = 0x1.555556p-5f, C6 = -0x1.6c16c2p-10f, C8 = 0x1.a01a02p-16f,
+                C10 = -0x1.27e4fcp-22f;
+// ln 2 in a 16-bit head and a float32 tail; log2(e).
+constexpr float LN2_HI = 0x1.62e4p-1f;
+constexpr float LN2_LO = 0x1.7f7d1cp-20f;
+constexpr float LOG2E = 0x1.715476p+0f;
+constexpr float E2 = 0x1p-1f, E3 = 0x1.555556p-3f, E4 = 0x1.555556p-5f, E5 = 0x1.111112p-7f,
+                E6 = 0x1.6c16c2p-10f, E7 = 0x1.a01a02p-13f, E8 = 0x1.a01a02p-16f;
+constexpr float TANH_CLAMP = 10.0f;
+}  // namespace dm
+
+__device__ __forceinline__ void det_sincos(float x, float* sin_out, float* cos_out) {
+  float r;
+  int q;
+  if (fabsf(x) <= dm::SMALL_ARG) {
+    const float k = rintf(x * dm::TWO_OVER_PI);
+    r = (((x - k * dm::PIO2_1) - k * dm::PIO2_2) - k * dm::PIO2_3) - k * dm::PIO2_4;
+    q = (int)k & 3;
+  } else {
+    const double xd = (double)x;
+    const double kd = rint(xd * dm::TWO_OVER_PI_D);
+    r = (float)((xd - kd * dm::PIO2_1D) - kd * dm::PIO2_2D);
+    const double qd = kd - 4.0 * floor(kd * 0.25);
+    q = (qd >= 0.0 && qd < 4.0) ? ((int)qd & 3) : 0;  // inf/NaN: quadrant 0, result NaN
+  }
+  const float z = r * r;
+  float sp = dm::S7 + z * dm::S9;
+  sp = dm::S5 + z * sp;
+  sp = dm::S3 + z * sp;
+  const float s = r + (r * z) * sp;
+  float cp = dm::C8 + z * dm::C10;
+  cp = dm::C6 + z * cp;
+  cp = dm::C4 + z * cp;
+  cp = dm::C2 + z * cp;
+  const float c = 1.0f + z * cp;
+  const float a = (q & 1) ? c : s;
+  const float b = (q & 1) ? s : c;
+  *sin_out = (q & 2) ? -a : a;
+  *cos_out = ((q + 1) & 2) ? -b : b;
+}
+
+__device__ __forceinline__ float det_sin(float x) {
+  float s, c;
+  det_sincos(x, &s, &c);
+  return s;
+}
+
+__device__ __forceinline__ float det_cos(float x) {
+  float s, c;
+  det_sincos(x, &s, &c);
+  return c;
+}
+
+__device__ __forceinline__ float det_tanh(float x) {
+  float a = fabsf(x);
+  a = (a > dm::TANH_CLAMP) ? dm::TANH_CLAMP : a;  // NaN compares false and stays NaN
+  const float y = a + a;
+  const float k = rintf(y * dm::LOG2E);
+  const float r = (y - k * dm::LN2_HI) - k * dm::LN2_LO;
+  float p = dm::E7 + r * dm::E8;
+  p = dm::E6 + r * p;
+  p = dm::E5 + r * p;
+  p = dm::E4 + r * p;
+  p = dm::E3 + r * p;
+  p = dm::E2 + r * p;
+  p = r + (r * r) * p;
+  const int ki = (k >= 0.0f && k <= 64.0f) ? (int)k : 0;
+  const float two_k = __int_as_float((ki + 127) << 23);
+  const float e = two_k * p + (two_k - 1.0f);
+  const float t = e / (e + 2.0f);
+  return copysignf(t, x);
+}
+
+// NaN-propagating clamp, numpy's np.clip semantics.
+__device__ __forceinline__ float clip(float v, float lo, float hi) {
+  v = (v < lo) ? lo : v;
+  return (v > hi) ? hi : v;
+}
+
+// ---------------------------------------------------------------------------
+// Launch geometry and C-ABI plumbing.
+// ---------------------------------------------------------------------------
+constexpr int kBlock = 256;
+
+inline unsigned grid_for(int64_t items, int block = kBlock) {
+  return (unsigned)((items + block - 1) / block);
+}
+
+void set_last_hip_error(int err);
+
+// Checks the launch just enqueued; returns HIPENVS_OK or HIPENVS_E_HIP.
+inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_hip_error((int)e);
+    return HIPENVS_E_HIP;
+  }
+  return HIPENVS_OK;
+}
+
+inline hipStream_t as_stream(hipenvs_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace hipenvs

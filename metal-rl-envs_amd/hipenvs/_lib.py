@@ -1,0 +1,138 @@
+"""ctypes binding of libhipenvs.so and the tensor checks shared by every module.
+
+The library is the product: every env step and rollout runs in it. Nothing here
+computes a result on the host; when the library is missing or no GPU is
+visible, the call raises instead of falling back to anything else.
+
+torch is imported before the library is opened so that the process holds one
+HIP runtime: libhipenvs.so's ``libamdhip64.so.7`` dependency binds to the
+runtime torch already loaded, and torch's stream handles are valid for it.
+"""
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).with_name("libhipenvs.so")
+
+OK, E_ARG, E_UNSUPPORTED, E_HIP = 0, -1, -2, -3
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_U32 = ctypes.c_uint32
+_F32 = ctypes.c_float
+
+# name -> argtypes, every entry point of include/hipenvs.h that returns a status int
+SIGNATURES = {
+    "hipenvs_cartpole_reset": [_P, _I64, _U32, _P],
+    "hipenvs_cartpole_step": [_P, _P, _U32, _P, _P, _P, _I64, _P],
+    "hipenvs_cartpole_step_k": [_P, _P, _U32, _I32, _P, _P, _P, _I64, _P],
+    "hipenvs_sample_actions": [_P, _I64, _I32, _U32, _P],
+    "hipenvs_detmath": [_P, _P, _P, _P, _I64, _P],
+}
+
+
+class HipEnvsError(RuntimeError):
+    """A failed hipenvs call: bad argument, unsupported shape, or a HIP launch error."""
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises HipEnvsError when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise HipEnvsError(f"{LIB_PATH} is missing; build it with `python metal-rl-envs_amd/build.py`")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        handle.hipenvs_version.restype = ctypes.c_char_p
+        handle.hipenvs_version.argtypes = []
+        handle.hipenvs_last_hip_error.restype = ctypes.c_int
+        handle.hipenvs_last_hip_error.argtypes = []
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    """Call entry point `name` and raise HipEnvsError on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != OK:
+        if rc == E_HIP:
+            raise HipEnvsError(f"{name}: HIP launch failed (hipError_t {lib().hipenvs_last_hip_error()})")
+        if rc == E_UNSUPPORTED:
+            raise HipEnvsError(f"{name}: no kernel instantiated for these compile-time parameters")
+        raise HipEnvsError(f"{name}: invalid argument (status {rc})")
+
+
+def version():
+    return lib().hipenvs_version().decode()
+
+
+# ---- tensor plumbing --------------------------------------------------------
+
+def default_device():
+    if not torch.cuda.is_available():
+        raise HipEnvsError("hipenvs needs a ROCm GPU: torch.cuda.is_available() is False")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def stream_of(device):
+    """hipStream_t handle of torch's current stream on `device`."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def check_state(state, rows, name="state"):
+    """A (rows, n) float32 contiguous tensor on a GPU; returns n."""
+    if not isinstance(state, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(state).__name__}")
+    if state.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {state.dtype}")
+    if state.dim() != 2 or state.shape[0] != rows:
+        raise ValueError(f"{name} must have shape ({rows}, n), got {tuple(state.shape)}")
+    if state.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm GPU, got device {state.device}")
+    if not state.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return state.shape[1]
+
+
+def as_actions(action, n, device, name="action"):
+    """An (n,) int32 contiguous device tensor; other integer dtypes are converted (one copy)."""
+    if not isinstance(action, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(action).__name__}")
+    if action.dtype.is_floating_point or action.dtype == torch.bool or action.dtype.is_complex:
+        raise TypeError(f"{name} must be an integer tensor, got {action.dtype}")
+    if action.shape != (n,):
+        raise ValueError(f"{name} must have shape ({n},), got {tuple(action.shape)}")
+    if action.device != device:
+        raise ValueError(f"{name} is on {action.device}, state is on {device}")
+    if action.dtype != torch.int32:
+        action = action.to(torch.int32)
+    return action.contiguous()
+
+
+def as_f32_vector(x, n, device, name):
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(x).__name__}")
+    if x.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {x.dtype}")
+    if x.shape != (n,):
+        raise ValueError(f"{name} must have shape ({n},), got {tuple(x.shape)}")
+    if x.device != device:
+        raise ValueError(f"{name} is on {x.device}, state is on {device}")
+    return x.contiguous()
+
+
+def u32(seed):
+    return ctypes.c_uint32(int(seed) & 0xFFFFFFFF)

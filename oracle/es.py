@@ -1,0 +1,62 @@
+"""Evolution-strategies pieces restated in numpy for the oracle.
+
+TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+
+* ``n_params`` / ``unflatten``: ``es.py:152-164``. A member's row is w1 (I, H)
+  row-major, b1 (H), w2 (H, O) row-major, b2 (O).
+* ``centered_ranks``: ``es.py:214-215`` with ties broken by index (a stable
+  sort on both sides), which the reference's quicksort-based argsort leaves
+  unspecified.
+* ``legged_action``: ``es.py:86-93``: per-leg first-index argmax of each
+  three-way head, composed as sum_k a_k 3**k.
+* ``loop_fitness``: ``es.py:174-193``: step the whole population once per
+  iteration with auto-reset, count ``steps += alive``, then
+  ``fit += (forward + alive_bonus) * alive - fall_penalty * fell``.
+"""
+
+import numpy as np
+
+F32 = np.float32
+
+
+def n_params(hidden, obs_dim, n_out):
+    return obs_dim * hidden + hidden + hidden * n_out + n_out
+
+
+def unflatten(theta_pop, hidden, obs_dim, n_out):
+    """(P, D) rows to (w1 (P, I, H), b1 (P, H), w2 (P, H, O), b2 (P, O)); ``es.py:156-164``."""
+    p, h, i, o = theta_pop.shape[0], hidden, obs_dim, n_out
+    k = 0
+    w1 = theta_pop[:, k:k + i * h].reshape(p, i, h); k += i * h
+    b1 = theta_pop[:, k:k + h]; k += h
+    w2 = theta_pop[:, k:k + h * o].reshape(p, h, o); k += h * o
+    b2 = theta_pop[:, k:k + o]
+    return w1, b1, w2, b2
+
+
+def centered_ranks(values):
+    """Ranks in [-0.5, 0.5], ties broken by index; ``es.py:214-215``."""
+    values = np.asarray(values)
+    order = np.argsort(values, kind="stable")
+    ranks = np.empty(values.shape[0], dtype=np.int64)
+    ranks[order] = np.arange(values.shape[0])
+    return ranks.astype(values.dtype) / (values.shape[0] - 1) - 0.5
+
+
+def first_argmax(logits):
+    """First-index argmax over axis 0 of a (m, P) stack, as the fused kernels' strict '>' chain."""
+    best = logits[0]
+    idx = np.zeros(best.shape, dtype=np.int32)
+    for j in range(1, logits.shape[0]):
+        better = logits[j] > best
+        idx = np.where(better, j, idx)
+        best = np.where(better, logits[j], best)
+    return idx
+
+
+def legged_action(logits, c):
+    """logits (P, 3C) -> action index sum_k argmax(logits[:, 3k:3k+3]) * 3**k; ``es.py:86-93``."""
+    out = np.zeros(logits.shape[0], dtype=np.int32)
+    for k in range(c):
+        out = out + np.argmax(logits[:, 3 * k:3 * k + 3], axis=-1).astype(np.int32) * 3**k
+    return out

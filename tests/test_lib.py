@@ -1,0 +1,84 @@
+"""The C-ABI library without a GPU: it loads, exports what the header declares, and
+its compiled-in constants are the float32 values of the reference's constants (CPU)."""
+
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hipenvs.h"
+CSRC = ROOT / "metal-rl-envs_amd" / "csrc"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(hipenvs_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from hipenvs import _lib
+
+    assert _lib.LIB_PATH.exists(), "run python metal-rl-envs_amd/build.py"
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    names = declared_functions()
+    assert len(names) >= 7
+    for name in names:
+        assert hasattr(handle, name), name
+
+
+def test_python_binding_covers_the_header():
+    from hipenvs import _lib
+
+    status_fns = set(declared_functions()) - {"hipenvs_version", "hipenvs_last_hip_error"}
+    assert status_fns == set(_lib.SIGNATURES)
+    assert _lib.version().startswith("hipenvs ")
+    assert _lib.lib().hipenvs_last_hip_error() == 0
+
+
+def test_bad_arguments_are_rejected_before_any_launch():
+    """The C ABI validates sizes and pointers; none of these reach the GPU."""
+    from hipenvs import _lib
+
+    l = _lib.lib()
+    null = ctypes.c_void_p(0)
+    assert l.hipenvs_cartpole_step(null, null, 0, null, null, null, 16, null) == _lib.E_ARG
+    assert l.hipenvs_cartpole_step(null, null, 0, null, null, null, -1, null) == _lib.E_ARG
+    assert l.hipenvs_cartpole_step(null, null, 0, null, null, null, 0, null) == _lib.OK
+    assert l.hipenvs_sample_actions(null, 8, 0, 0, null) == _lib.E_ARG
+    assert l.hipenvs_sample_actions(null, 8, 257, 0, null) == _lib.E_ARG
+
+
+def test_python_wrappers_check_tensors():
+    import torch
+
+    from hipenvs import cartpole
+
+    with pytest.raises(TypeError):
+        cartpole.step(np.zeros((4, 8), np.float32), torch.zeros(8, dtype=torch.int32))
+    with pytest.raises(TypeError):
+        cartpole.step(torch.zeros((4, 8), dtype=torch.float64), torch.zeros(8, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        cartpole.step(torch.zeros((3, 8)), torch.zeros(8, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        cartpole.step(torch.zeros((4, 8)), torch.zeros(8, dtype=torch.int32))   # CPU tensor: not on a GPU
+
+
+def kernel_constants():
+    """(name, value, expression) for every `constexpr float NAME = HEX;  // float32(EXPR)` line."""
+    out = []
+    for path in sorted(CSRC.glob("*.hip")):
+        for m in re.finditer(r"constexpr float (\w+) = (-?0x[0-9a-fA-F.]+p[+-]?\d+)f;\s*// float32\((.+)\)", path.read_text()):
+            out.append((f"{path.name}:{m.group(1)}", float.fromhex(m.group(2)), m.group(3)))
+    return out
+
+
+def test_kernel_constants_are_float32_of_the_reference_values():
+    consts = kernel_constants()
+    assert len(consts) >= 11
+    for name, value, expr in consts:
+        expect = float(np.float32(eval(expr, {"pi": math.pi, "np": np})))
+        assert value == expect, (name, expr, value, expect)
