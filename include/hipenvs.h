@@ -77,6 +77,43 @@ int hipenvs_cartpole_step_k(const float* state, const int32_t* actions, uint32_t
  * mx.random.randint inside the loop). */
 int hipenvs_sample_actions(int32_t* action, int64_t n, int32_t m, uint32_t seed, hipenvs_stream_t stream);
 
+/* Fused ES rollout on CartPole: one thread per member runs its own 4-H-2 tanh
+ * policy (row i of theta (p, 7*hidden+2) in es.unflatten's layout: w1 (4, H)
+ * row-major, b1 (H), w2 (H, 2) row-major, b2 (2)) from state (4, p) for up to
+ * `horizon` steps and writes the steps survived before its first termination
+ * (the terminating step not counted) to fitness (p) f32. No auto-reset, no RNG.
+ * hidden in {4, 8, 16, 32, 64}.
+ * Replaces the `cartpole_es_rollout` Metal kernel and
+ * cartpole_rollout_metal.rollout_steps (cartpole_rollout_metal.py:46-100). */
+int hipenvs_cartpole_es_rollout(const float* state, const float* theta, int64_t p, int32_t hidden,
+                                int32_t horizon, float* fitness, hipenvs_stream_t stream);
+
+/* ---- Acrobot ----------------------------------------------------------- */
+
+/* Fresh states (4, n) uniform in +-0.1 at counter `seed`.
+ * Replaces acrobot_mlx.reset, re-exported by acrobot_metal.py:8. */
+int hipenvs_acrobot_reset(float* state, int64_t n, uint32_t seed, hipenvs_stream_t stream);
+
+/* One Gym Acrobot step (book dynamics, RK4 dt 0.2, wrap, clip) with masked
+ * auto-reset. state (4, n) f32 rows theta1, theta2, dtheta1, dtheta2; action (n)
+ * i32 in {0, 1, 2} (torque action - 1) -> next_state (4, n), reward (n) f32
+ * (-1, or 0 on done), done (n) u8.
+ * Replaces the `acrobot_step` Metal kernel and acrobot_metal.step
+ * (acrobot_metal.py:57-111). */
+int hipenvs_acrobot_step(const float* state, const int32_t* action, uint32_t seed,
+                         float* next_state, float* reward, uint8_t* done,
+                         int64_t n, hipenvs_stream_t stream);
+
+/* Fused ES rollout on Acrobot: 6-H-3 tanh policy on (cos th1, sin th1, cos th2,
+ * sin th2, dth1, dth2), first-index argmax over torques (-1, 0, +1); theta is
+ * (p, 10*hidden+3) in es.unflatten's layout. Writes the steps taken before the
+ * tip first clears height 1 (horizon if never) to steps (p) f32.
+ * hidden in {4, 8, 16, 32, 64}.
+ * Replaces the `acrobot_es_rollout` Metal kernel and
+ * acrobot_rollout_metal.rollout_steps (acrobot_rollout_metal.py:21-81). */
+int hipenvs_acrobot_es_rollout(const float* state, const float* theta, int64_t p, int32_t hidden,
+                               int32_t horizon, float* steps, hipenvs_stream_t stream);
+
 /* ---- Diagnostics (no reference counterpart) ---------------------------- */
 
 /* Elementwise deterministic sin, cos, tanh of x (n) as the kernels compute them;

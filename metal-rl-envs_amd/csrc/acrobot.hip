@@ -1,0 +1,195 @@
+// Acrobot on MI355X: the single-step kernel (RK4 at dt 0.2, wrap, clip, masked
+// reset) and the fused ES rollout kernel (6-H-3 tanh policy + the same physics
+// for the whole horizon in registers), with their C-ABI entry points.
+//
+// The derivative follows acrobot_np.py:64-84 operation by operation, with the
+// Python-scalar products already folded to the float32 constants numpy uses
+// (each constant's defining expression is beside it); RK4/wrap/clip follow
+// acrobot_np.py:47-61,87-89, termination acrobot_np.py:92-93, reset the
+// counter RNG of acrobot_metal.py:78-83. Per env-step the step kernel moves 41
+// algorithmic bytes; it is VALU-bound (14 sin/cos, 18 IEEE divisions).
+
+#include "hipenvs_device.h"
+
+namespace hipenvs {
+namespace ac {
+
+constexpr float D1_C0 = 0x1p-2f;              // float32(1.0 * 0.5**2)
+constexpr float D1_C1 = 0x1.4p+0f;            // float32(1.0**2 + 0.5**2)
+constexpr float D2_C0 = 0x1p-2f;              // float32(0.5**2)
+constexpr float D2_C1 = 0x1p-1f;              // float32(1.0 * 0.5)
+constexpr float PHI2_C = 0x1.39999ap+2f;      // float32(1.0 * 0.5 * 9.8)
+constexpr float HALF_PI = 0x1.921fb6p+0f;     // float32(pi / 2)
+constexpr float PHI1_A = -0x1p-1f;            // float32(-1.0 * 1.0 * 0.5)
+constexpr float PHI1_C = 0x1.d66666p+3f;      // float32((1.0 * 0.5 + 1.0 * 1.0) * 9.8)
+constexpr float DD2_C = 0x1p-1f;              // float32(1.0 * 1.0 * 0.5)
+constexpr float DEN_C = 0x1.4p+0f;            // float32(1.0 * 0.5**2 + 1.0)
+constexpr float DT = 0x1.99999ap-3f;          // float32(0.2)
+constexpr float DT_2 = 0x1.99999ap-4f;        // float32(0.2 / 2)
+constexpr float DT_6 = 0x1.111112p-5f;        // float32(0.2 / 6)
+constexpr float TWO_PI = 0x1.921fb6p+2f;      // float32(2 * pi)
+constexpr float PI = 0x1.921fb6p+1f;          // float32(pi)
+constexpr float MAX_VEL_1 = 0x1.921fb6p+3f;   // float32(4 * pi)
+constexpr float MAX_VEL_2 = 0x1.c463acp+4f;   // float32(9 * pi)
+constexpr float RESET_BOUND = 0x1.99999ap-4f; // float32(0.1)
+
+struct S4 {
+  float a, b, c, d;  // theta1, theta2, dtheta1, dtheta2 (or their derivatives)
+};
+
+// acrobot_np.py:64-84. The numpy expression's multiplications by the Python
+// float 1.0 (m2 *, 2 * l1 * lc2 *) are exact and omitted.
+__device__ __forceinline__ S4 dsdt(const S4& s, float torque) {
+  float s2, c2;
+  det_sincos(s.b, &s2, &c2);
+  const float d1 = ((D1_C0 + (D1_C1 + c2)) + 1.0f) + 1.0f;
+  const float d2 = (D2_C0 + D2_C1 * c2) + 1.0f;
+  const float phi2 = PHI2_C * det_cos((s.a + s.b) - HALF_PI);
+  const float t1 = (PHI1_A * (s.d * s.d)) * s2;
+  const float t2 = (s.d * s.c) * s2;
+  const float t3 = PHI1_C * det_cos(s.a - HALF_PI);
+  const float phi1 = ((t1 - t2) + t3) + phi2;
+  const float num = ((torque + (d2 / d1) * phi1) - (DD2_C * (s.c * s.c)) * s2) - phi2;
+  const float den = DEN_C - (d2 * d2) / d1;
+  const float dd2 = num / den;
+  const float dd1 = (-((d2 * dd2) + phi1)) / d1;
+  return S4{s.c, s.d, dd1, dd2};
+}
+
+__device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf((x + PI) / TWO_PI); }
+
+// RK4 + wrap + clip in place (acrobot_np.py:47-61).
+__device__ __forceinline__ void rk4(S4& s, float torque) {
+  const S4 k1 = dsdt(s, torque);
+  const S4 k2 = dsdt(S4{s.a + DT_2 * k1.a, s.b + DT_2 * k1.b, s.c + DT_2 * k1.c, s.d + DT_2 * k1.d}, torque);
+  const S4 k3 = dsdt(S4{s.a + DT_2 * k2.a, s.b + DT_2 * k2.b, s.c + DT_2 * k2.c, s.d + DT_2 * k2.d}, torque);
+  const S4 k4 = dsdt(S4{s.a + DT * k3.a, s.b + DT * k3.b, s.c + DT * k3.c, s.d + DT * k3.d}, torque);
+  const float na = s.a + DT_6 * (((k1.a + 2.0f * k2.a) + 2.0f * k3.a) + k4.a);
+  const float nb = s.b + DT_6 * (((k1.b + 2.0f * k2.b) + 2.0f * k3.b) + k4.b);
+  const float nc = s.c + DT_6 * (((k1.c + 2.0f * k2.c) + 2.0f * k3.c) + k4.c);
+  const float nd = s.d + DT_6 * (((k1.d + 2.0f * k2.d) + 2.0f * k3.d) + k4.d);
+  s.a = wrap(na);
+  s.b = wrap(nb);
+  s.c = clip(nc, -MAX_VEL_1, MAX_VEL_1);
+  s.d = clip(nd, -MAX_VEL_2, MAX_VEL_2);
+}
+
+// acrobot_np.py:92-93: -cos(th1) - cos(th2 + th1) > 1.
+__device__ __forceinline__ bool terminal(const S4& s) { return (-det_cos(s.a)) - det_cos(s.b + s.a) > 1.0f; }
+
+__global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state, uint32_t seed, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t h = env_hash(seed, (uint32_t)i);
+  state[i] = uniform_pm(pcg_hash(h), RESET_BOUND);
+  state[n + i] = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
+  state[2 * n + i] = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
+  state[3 * n + i] = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
+}
+
+__global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ state, const int32_t* __restrict__ action,
+                                                      uint32_t seed, float* __restrict__ next, float* __restrict__ reward,
+                                                      uint8_t* __restrict__ done, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  S4 s{state[i], state[n + i], state[2 * n + i], state[3 * n + i]};
+  const float torque = (float)(action[i] - 1);
+  rk4(s, torque);
+  const bool d = terminal(s);
+  const uint32_t h = env_hash(seed, (uint32_t)i);
+  const float f0 = uniform_pm(pcg_hash(h), RESET_BOUND);
+  const float f1 = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
+  const float f2 = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
+  const float f3 = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
+  next[i] = d ? f0 : s.a;
+  next[n + i] = d ? f1 : s.b;
+  next[2 * n + i] = d ? f2 : s.c;
+  next[3 * n + i] = d ? f3 : s.d;
+  reward[i] = d ? 0.0f : -1.0f;
+  done[i] = d ? 1 : 0;
+}
+
+// Fused ES rollout: one thread per member, the member's 10H+3 weights in
+// registers (es.unflatten layout: w1 (6, H), b1 (H), w2 (H, 3), b2 (3)),
+// Gym's observation, first-index argmax over three torques, RK4 physics, stop
+// at the first termination. acrobot_rollout_metal.py:21-58.
+template <int H>
+__global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
+                                                     int64_t p, int32_t horizon, float* __restrict__ steps_out) {
+  constexpr int D = 10 * H + 3;
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (i >= p) return;
+  const float* row = theta + i * D;
+  float w[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) w[d] = row[d];
+  S4 s{state[i], state[p + i], state[2 * p + i], state[3 * p + i]};
+  float steps = 0.0f;
+  for (int32_t t = 0; t < horizon; ++t) {
+    float o[6];
+    det_sincos(s.a, &o[1], &o[0]);
+    det_sincos(s.b, &o[3], &o[2]);
+    o[4] = s.c;
+    o[5] = s.d;
+    float l0 = w[10 * H], l1 = w[10 * H + 1], l2 = w[10 * H + 2];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+      float pre = o[0] * w[j];
+#pragma unroll
+      for (int k = 1; k < 6; ++k) pre = pre + o[k] * w[k * H + j];
+      const float h = det_tanh(pre + w[6 * H + j]);
+      l0 = l0 + h * w[7 * H + 3 * j];
+      l1 = l1 + h * w[7 * H + 3 * j + 1];
+      l2 = l2 + h * w[7 * H + 3 * j + 2];
+    }
+    float torque = -1.0f, best = l0;
+    if (l1 > best) { torque = 0.0f; best = l1; }
+    if (l2 > best) { torque = 1.0f; }
+    rk4(s, torque);
+    if (terminal(s)) break;
+    steps += 1.0f;
+  }
+  steps_out[i] = steps;
+}
+
+template <int H>
+int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+  return launch_status();
+}
+
+}  // namespace ac
+}  // namespace hipenvs
+
+using namespace hipenvs;
+
+extern "C" int hipenvs_acrobot_reset(float* state, int64_t n, uint32_t seed, hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && !state)) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipLaunchKernelGGL(ac::reset_kernel, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), state, seed, n);
+  return launch_status();
+}
+
+extern "C" int hipenvs_acrobot_step(const float* state, const int32_t* action, uint32_t seed, float* next_state,
+                                    float* reward, uint8_t* done, int64_t n, hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !action || !next_state || !reward || !done))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipLaunchKernelGGL(ac::step_kernel, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), state, action, seed,
+                     next_state, reward, done, n);
+  return launch_status();
+}
+
+extern "C" int hipenvs_acrobot_es_rollout(const float* state, const float* theta, int64_t p, int32_t hidden,
+                                          int32_t horizon, float* steps, hipenvs_stream_t stream) {
+  if (p < 0 || horizon < 0 || (p > 0 && (!state || !theta || !steps))) return HIPENVS_E_ARG;
+  if (p == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  switch (hidden) {
+    case 4: return ac::launch_rollout<4>(state, theta, p, horizon, steps, s);
+    case 8: return ac::launch_rollout<8>(state, theta, p, horizon, steps, s);
+    case 16: return ac::launch_rollout<16>(state, theta, p, horizon, steps, s);
+    case 32: return ac::launch_rollout<32>(state, theta, p, horizon, steps, s);
+    case 64: return ac::launch_rollout<64>(state, theta, p, horizon, steps, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}

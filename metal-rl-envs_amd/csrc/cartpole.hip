@@ -194,6 +194,44 @@ __global__ __launch_bounds__(kBlock) void detmath_kernel(const float* __restrict
   th[i] = det_tanh(x[i]);
 }
 
+// Fused ES rollout: one thread per member, the member's 7H+2 weights in
+// registers (es.unflatten layout: w1 (4, H), b1 (H), w2 (H, 2), b2 (2)), the
+// 4-H-2 tanh policy with first-index argmax, the step physics, and an early
+// exit at the first termination; writes the steps survived (the terminating
+// step not counted). cartpole_rollout_metal.py:46-77.
+template <int H>
+__global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
+                                                     int64_t p, int32_t horizon, float* __restrict__ fitness) {
+  constexpr int D = 7 * H + 2;
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (i >= p) return;
+  const float* row = theta + i * D;
+  float w[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) w[d] = row[d];
+  float x = state[i], xd = state[p + i], th = state[2 * p + i], thd = state[3 * p + i];
+  float survived = 0.0f;
+  for (int32_t t = 0; t < horizon; ++t) {
+    float l0 = w[7 * H], l1 = w[7 * H + 1];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+      const float pre = (((x * w[j] + xd * w[H + j]) + th * w[2 * H + j]) + thd * w[3 * H + j]) + w[4 * H + j];
+      const float h = det_tanh(pre);
+      l0 = l0 + h * w[5 * H + 2 * j];
+      l1 = l1 + h * w[5 * H + 2 * j + 1];
+    }
+    if (advance(x, xd, th, thd, (l1 > l0) ? 1 : 0)) break;
+    survived += 1.0f;
+  }
+  fitness[i] = survived;
+}
+
+template <int H>
+int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+  return launch_status();
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace cp
@@ -266,4 +304,19 @@ extern "C" int hipenvs_detmath(const float* x, float* sin_out, float* cos_out, f
   hipLaunchKernelGGL(cp::detmath_kernel, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), x, sin_out, cos_out,
                      tanh_out, n);
   return launch_status();
+}
+
+extern "C" int hipenvs_cartpole_es_rollout(const float* state, const float* theta, int64_t p, int32_t hidden,
+                                           int32_t horizon, float* fitness, hipenvs_stream_t stream) {
+  if (p < 0 || horizon < 0 || (p > 0 && (!state || !theta || !fitness))) return HIPENVS_E_ARG;
+  if (p == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  switch (hidden) {
+    case 4: return cp::launch_rollout<4>(state, theta, p, horizon, fitness, s);
+    case 8: return cp::launch_rollout<8>(state, theta, p, horizon, fitness, s);
+    case 16: return cp::launch_rollout<16>(state, theta, p, horizon, fitness, s);
+    case 32: return cp::launch_rollout<32>(state, theta, p, horizon, fitness, s);
+    case 64: return cp::launch_rollout<64>(state, theta, p, horizon, fitness, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
 }

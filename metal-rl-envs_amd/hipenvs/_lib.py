@@ -31,6 +31,10 @@ SIGNATURES = {
     "hipenvs_cartpole_step_k": [_P, _P, _U32, _I32, _P, _P, _P, _I64, _P],
     "hipenvs_sample_actions": [_P, _I64, _I32, _U32, _P],
     "hipenvs_detmath": [_P, _P, _P, _P, _I64, _P],
+    "hipenvs_cartpole_es_rollout": [_P, _P, _I64, _I32, _I32, _P, _P],
+    "hipenvs_acrobot_reset": [_P, _I64, _U32, _P],
+    "hipenvs_acrobot_step": [_P, _P, _U32, _P, _P, _P, _I64, _P],
+    "hipenvs_acrobot_es_rollout": [_P, _P, _I64, _I32, _I32, _P, _P],
 }
 
 
@@ -136,3 +140,56 @@ def as_f32_vector(x, n, device, name):
 
 def u32(seed):
     return ctypes.c_uint32(int(seed) & 0xFFFFFFFF)
+
+
+# ---- shared launch helpers of the step and rollout modules -------------------
+
+def launch_reset(entry, rows, n, seed, device):
+    """A fresh (rows, n) state from reset entry point `entry` at counter `seed`."""
+    state = torch.empty((rows, n), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        call(entry, ptr(state), n, u32(seed), stream_of(device))
+    return state
+
+
+def launch_step(entry, rows, state, action, seed, *extra):
+    """(next_state, reward, done) of step entry point `entry`; `extra` C arguments go
+    between the seed and the output pointers."""
+    n = check_state(state, rows)
+    device = state.device
+    action = as_actions(action, n, device)
+    next_state = torch.empty_like(state)
+    reward = torch.empty(n, dtype=torch.float32, device=device)
+    done = torch.empty(n, dtype=torch.bool, device=device)
+    with torch.cuda.device(device):
+        call(entry, ptr(state), ptr(action), u32(seed), *extra, ptr(next_state), ptr(reward), ptr(done), n,
+             stream_of(device))
+    return next_state, reward, done
+
+
+def check_theta(theta_pop, p, d, device, name="theta_pop"):
+    """A (p, d) float32 contiguous device tensor (es.unflatten's row layout)."""
+    if not isinstance(theta_pop, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(theta_pop).__name__}")
+    if theta_pop.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {theta_pop.dtype}")
+    if theta_pop.shape != (p, d):
+        raise ValueError(f"{name} must have shape ({p}, {d}), got {tuple(theta_pop.shape)}")
+    if theta_pop.device != device:
+        raise ValueError(f"{name} is on {theta_pop.device}, state is on {device}")
+    return theta_pop.contiguous()
+
+
+HIDDEN_SIZES = (4, 8, 16, 32, 64)
+
+
+def check_hidden(hidden):
+    if int(hidden) not in HIDDEN_SIZES:
+        raise ValueError(f"hidden must be one of {HIDDEN_SIZES}, got {hidden}")
+    return int(hidden)
+
+
+def check_horizon(horizon):
+    if int(horizon) < 0:
+        raise ValueError("horizon must be >= 0")
+    return int(horizon)

@@ -1,0 +1,30 @@
+"""The whole Acrobot ES rollout as one kernel launch: drop-in for the reference's
+``acrobot_rollout_metal`` module (``acrobot_rollout_metal.py:69-81``).
+
+Each of P members runs its own 6-H-3 tanh MLP policy on Gym's observation
+(cos and sin of both angles, both velocities) against the RK4 physics and
+returns the steps taken before the tip first clears height 1 (the horizon if it
+never does).
+"""
+
+import torch
+
+from . import _lib
+
+
+def n_params(hidden):
+    return 10 * hidden + 3
+
+
+def rollout_steps(state, theta_pop, hidden, horizon):
+    """Steps before the first termination for each of P members from `state` (4, P),
+    each with its own policy row of `theta_pop` (P, 10*hidden+3). Returns (P,) float32."""
+    p = _lib.check_state(state, 4)
+    hidden = _lib.check_hidden(hidden)
+    horizon = _lib.check_horizon(horizon)
+    theta_pop = _lib.check_theta(theta_pop, p, n_params(hidden), state.device)
+    steps = torch.empty(p, dtype=torch.float32, device=state.device)
+    with torch.cuda.device(state.device):
+        _lib.call("hipenvs_acrobot_es_rollout", _lib.ptr(state), _lib.ptr(theta_pop), p, hidden, horizon,
+                  _lib.ptr(steps), _lib.stream_of(state.device))
+    return steps

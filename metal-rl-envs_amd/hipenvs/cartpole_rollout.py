@@ -1,0 +1,29 @@
+"""The whole CartPole ES rollout as one kernel launch: drop-in for the reference's
+``cartpole_rollout_metal`` module (``cartpole_rollout_metal.py:88-100``).
+
+Each of P members runs its own 4-H-2 tanh MLP policy (row of ``theta_pop`` in
+``es.unflatten``'s layout) against the CartPole physics for the full horizon in
+registers and returns the steps it survived before its first termination.
+"""
+
+import torch
+
+from . import _lib
+
+
+def n_params(hidden):
+    return 7 * hidden + 2
+
+
+def rollout_steps(state, theta_pop, hidden, horizon):
+    """Steps survived by each of P members from `state` (4, P), each with its own
+    policy row of `theta_pop` (P, 7*hidden+2); asynchronous. Returns (P,) float32."""
+    p = _lib.check_state(state, 4)
+    hidden = _lib.check_hidden(hidden)
+    horizon = _lib.check_horizon(horizon)
+    theta_pop = _lib.check_theta(theta_pop, p, n_params(hidden), state.device)
+    fitness = torch.empty(p, dtype=torch.float32, device=state.device)
+    with torch.cuda.device(state.device):
+        _lib.call("hipenvs_cartpole_es_rollout", _lib.ptr(state), _lib.ptr(theta_pop), p, hidden, horizon,
+                  _lib.ptr(fitness), _lib.stream_of(state.device))
+    return fitness

@@ -1,0 +1,326 @@
+"""Evolution strategies on the batched HIP environments: the caller of the fused rollouts.
+
+A torch restatement of the reference's learner ``es.py`` (Salimans et al.
+2017): each population member is a small MLP with its own weights, the whole
+population runs against the batched environment for a horizon, and the update
+is a rank-weighted sum of antithetic perturbations, once per generation.
+
+Kept from the reference:
+
+* the task registry and per-task policy shapes (``es.py:47-132``);
+* the (P, D) parameter-row layout of ``n_params``/``unflatten``
+  (``es.py:152-164``): w1 (I, H), b1 (H), w2 (H, O), b2 (O), row-major;
+* ``loop_fitness``'s accounting (``es.py:174-193``), ``push``/``curriculum``
+  (``es.py:196-211``), ``centered_ranks`` (``es.py:214-215``, with ties broken
+  by index: a stable sort), ``generation`` (``es.py:218-227``), ``evaluate``
+  (``es.py:308-322``) and ``train`` (``es.py:334-354``).
+
+Backends (``es.py:230-299``): ``"fused"`` runs the whole rollout as one HIP
+launch per generation (the reference's ``metal`` backend); ``"loop"`` runs the
+policy in torch and steps the HIP step kernel once per iteration (its ``mlx``
+backend). The reference's ``numpy`` backend is the CPU oracle, which this
+package does not import. Sampling, ranking and the update are torch ops on the
+GPU.
+"""
+
+import argparse
+import time
+from dataclasses import dataclass
+from typing import Any, Callable
+
+import torch
+
+from . import acrobot, acrobot_rollout, cartpole, cartpole_rollout
+
+
+@dataclass(frozen=True)
+class Task:
+    name: str
+    obs_dim: int
+    n_out: int
+    hidden: int
+    solved_at: float
+    env: Any                   # step module/object: reset(n, seed=None, device=None), step(state, action[, assist])
+    obs: Callable              # state (D, P) -> (P, obs_dim)
+    action: Callable           # logits (P, n_out) -> action index (P,) int32
+    rollout: Callable          # (state, theta_pop, hidden, horizon[, assist]) -> (fitness, steps taken)
+    alive_bonus: float = 1.0
+    fall_penalty: float = 0.0
+    eval_bonus: float = 1.0
+    height_gate: float = 0.0
+    xdot_row: int | None = None
+    assistable: bool = False
+
+
+def argmax_action(logits):
+    return torch.argmax(logits, dim=-1).to(torch.int32)
+
+
+def cartpole_obs(state):
+    return state.T
+
+
+def acrobot_obs(state):
+    th1, th2, dth1, dth2 = state
+    return torch.stack([torch.cos(th1), torch.sin(th1), torch.cos(th2), torch.sin(th2), dth1, dth2], dim=1)
+
+
+def legged_obs(state):
+    """Everything but x: the policy is translation-invariant (``es.py:81-83``)."""
+    return state[1:].T
+
+
+def legged_action(c):
+    """Per-leg argmax of each three-way head, composed as sum_k a_k 3**k (``es.py:86-93``)."""
+    def action(logits):
+        out = torch.zeros(logits.shape[0], dtype=torch.int32, device=logits.device)
+        for k in range(c):
+            out = out + torch.argmax(logits[:, 3 * k:3 * k + 3], dim=-1).to(torch.int32) * 3**k
+        return out
+    return action
+
+
+def steps_fitness(kernel, sign):
+    """CartPole's and Acrobot's fused kernels return steps survived; fitness is that with the
+    task's sign and steps taken counts the terminating step, capped at the horizon (``es.py:96-103``)."""
+    def rollout(state, theta_pop, hidden, horizon):
+        steps = kernel(state, theta_pop, hidden, horizon)
+        return sign * steps, torch.clamp(steps + 1, max=horizon)
+    return rollout
+
+
+TASKS = {
+    "cartpole": Task("cartpole", 4, 2, 32, 475.0, cartpole, cartpole_obs, argmax_action,
+                     steps_fitness(cartpole_rollout.rollout_steps, 1.0)),
+    "acrobot": Task("acrobot", 6, 3, 32, -100.0, acrobot, acrobot_obs, argmax_action,
+                    steps_fitness(acrobot_rollout.rollout_steps, -1.0)),
+}
+
+
+def register(task):
+    TASKS[task.name] = task
+    return task
+
+
+@dataclass
+class Config:
+    task: str = "cartpole"
+    pop: int = 1024
+    hidden: int | None = None
+    sigma: float = 0.1
+    lr: float = 0.1
+    horizon: int = 500
+    solved_at: float | None = None
+    max_generations: int = 500
+    time_budget: float = 120.0
+    assist_k0: float = 0.0
+    start_velocity: float = 0.0
+    anneal_gens: int = 300
+
+
+def n_params(hidden, task):
+    return task.obs_dim * hidden + hidden + hidden * task.n_out + task.n_out
+
+
+def unflatten(theta_pop, hidden, task):
+    """(P, D) rows to (w1 (P, I, H), b1 (P, H), w2 (P, H, O), b2 (P, O)) views."""
+    p, h, i, o = theta_pop.shape[0], hidden, task.obs_dim, task.n_out
+    k = 0
+    w1 = theta_pop[:, k:k + i * h].reshape(p, i, h); k += i * h
+    b1 = theta_pop[:, k:k + h]; k += h
+    w2 = theta_pop[:, k:k + h * o].reshape(p, h, o); k += h * o
+    b2 = theta_pop[:, k:k + o]
+    return w1, b1, w2, b2
+
+
+def population_logits(obs, params):
+    """Every member runs its own policy (``es.py:167-171``), as elementwise products summed
+    over the input axis (float32 throughout)."""
+    w1, b1, w2, b2 = params
+    h = torch.tanh((obs[:, :, None] * w1).sum(dim=1) + b1)
+    return (h[:, :, None] * w2).sum(dim=1) + b2
+
+
+def push(task, state, start_velocity):
+    """The starting-push curriculum: a forward velocity added to every initial state (``es.py:196-205``)."""
+    if not start_velocity or task.xdot_row is None:
+        return state
+    state = state.clone()
+    state[task.xdot_row] += start_velocity
+    return state
+
+
+def curriculum(cfg, gen):
+    """Assistance stiffness and starting push at generation `gen` (``es.py:208-211``)."""
+    ramp = max(0.0, 1.0 - (gen - 1) / cfg.anneal_gens) if cfg.anneal_gens > 0 else 0.0
+    return cfg.assist_k0 * ramp, cfg.start_velocity * ramp
+
+
+def centered_ranks(values):
+    """argsort(argsort(v)) / (P - 1) - 0.5 with index tie-break (``es.py:214-215``)."""
+    order = torch.argsort(values, stable=True)
+    ranks = torch.empty_like(order)
+    ranks[order] = torch.arange(values.shape[0], device=values.device)
+    return ranks.to(values.dtype) / (values.shape[0] - 1) - 0.5
+
+
+class FusedBackend:
+    """One HIP launch per generation for the whole rollout (the reference's ``metal`` backend)."""
+
+    name = "fused"
+
+    def __init__(self, task, seed, device=None):
+        self.task = task
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.gen = torch.Generator(device=self.device)
+        self.gen.manual_seed(seed)
+        self.reset_counter = (seed * 0x01000193) & 0x7FFFFFFF
+        env = task.env
+        (env.reseed if hasattr(env, "reseed") else lambda s: None)(seed)
+
+    def normal(self, shape):
+        return torch.randn(shape, generator=self.gen, device=self.device, dtype=torch.float32)
+
+    def reset(self, n):
+        self.reset_counter += 1
+        return self.task.env.reset(n, seed=0xC0000000 + self.reset_counter, device=self.device)
+
+    def step(self, state, action, assist=None):
+        if assist is None:
+            return self.task.env.step(state, action)
+        return self.task.env.step(state, action, float(assist))
+
+    def rollout(self, theta_pop, hidden, horizon, assist=0.0, start_velocity=0.0):
+        state = push(self.task, self.reset(theta_pop.shape[0]), start_velocity)
+        if self.task.assistable:
+            return self.task.rollout(state, theta_pop, hidden, horizon, assist)
+        return self.task.rollout(state, theta_pop, hidden, horizon)
+
+
+class LoopBackend(FusedBackend):
+    """Policy in torch, one HIP step launch per iteration (the reference's ``mlx`` backend)."""
+
+    name = "loop"
+
+    def rollout(self, theta_pop, hidden, horizon, assist=0.0, start_velocity=0.0):
+        return loop_fitness(self, unflatten(theta_pop, hidden, self.task), horizon, assist, start_velocity)
+
+
+BACKENDS = {"fused": FusedBackend, "loop": LoopBackend}
+
+
+def loop_fitness(backend, params, horizon, assist=0.0, start_velocity=0.0, state=None):
+    """(reward sum until first termination, steps taken) per member, stepping the whole
+    population once per iteration with auto-reset (``es.py:174-193``)."""
+    task = backend.task
+    p = params[0].shape[0]
+    if state is None:
+        state = push(task, backend.reset(p), start_velocity)
+    alive = torch.ones(p, dtype=torch.bool, device=state.device)
+    fit = torch.zeros(p, device=state.device)
+    steps = torch.zeros(p, device=state.device)
+    for _ in range(horizon):
+        action = task.action(population_logits(task.obs(state), params))
+        state, reward, done = backend.step(state, action, assist) if task.assistable else backend.step(state, action)
+        steps = steps + alive.to(steps.dtype)
+        fell = alive & done
+        alive = alive & ~done
+        if task.height_gate:
+            forward = (reward - 1.0) * (state[1] >= task.height_gate).to(fit.dtype)
+        else:
+            forward = reward - 1.0
+        fit = fit + (forward + task.alive_bonus) * alive.to(fit.dtype) - task.fall_penalty * fell.to(fit.dtype)
+    return fit, steps
+
+
+def generation(backend, theta, cfg, hidden, gen=1):
+    """One ES generation (``es.py:218-227``): antithetic noise, rollout, ranks, update."""
+    half = backend.normal((cfg.pop // 2, theta.shape[0]))
+    eps = torch.cat([half, -half], dim=0)
+    assist, start_velocity = curriculum(cfg, gen)
+    fit, steps = backend.rollout(theta[None, :] + cfg.sigma * eps, hidden, cfg.horizon, assist, start_velocity)
+    grad = (centered_ranks(fit)[:, None] * eps).sum(dim=0) / (cfg.pop * cfg.sigma)
+    return theta + cfg.lr * grad, fit, steps
+
+
+def mean_policy(theta, hidden, task):
+    """The unperturbed policy as an actor on (n, obs_dim) observations (``es.py:302-305``)."""
+    w1, b1, w2, b2 = (p[0] for p in unflatten(theta[None, :], hidden, task))
+    return lambda obs: torch.tanh(obs @ w1 + b1) @ w2 + b2
+
+
+def evaluate(task, actor, n=2048, steps=500, device=None, seed=0x7FFF0000):
+    """Canonical score of a greedy actor over n fresh episodes: the environment's reward minus
+    one plus ``task.eval_bonus``, summed to the first termination (``es.py:308-322``)."""
+    device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    state = task.env.reset(n, seed=seed, device=device)
+    alive = torch.ones(n, dtype=torch.bool, device=device)
+    fit = torch.zeros(n, device=device)
+    for _ in range(steps):
+        action = task.action(actor(task.obs(state)))
+        state, reward, done = task.env.step(state, action)
+        alive = alive & ~done
+        fit = fit + (reward - 1.0 + task.eval_bonus) * alive.to(torch.float32)
+    return fit.mean().item()
+
+
+@dataclass
+class Result:
+    solved: bool
+    generations: int
+    env_steps: int
+    train_seconds: float
+    score: float
+
+
+def train(cfg, backend_name, seed, log=lambda *_: None, device=None):
+    """Generations until the mean policy's score reaches the threshold or the time budget
+    runs out (``es.py:334-354``); evaluation is outside the clock."""
+    assert cfg.pop % 2 == 0
+    task = TASKS[cfg.task]
+    hidden = task.hidden if cfg.hidden is None else cfg.hidden
+    solved_at = task.solved_at if cfg.solved_at is None else cfg.solved_at
+    backend = BACKENDS[backend_name](task, seed, device)
+    theta = backend.normal((n_params(hidden, task),)) * 0.1
+    train_seconds, env_steps, score, gen = 0.0, 0, 0.0, 0
+    for gen in range(1, cfg.max_generations + 1):
+        torch.cuda.synchronize(backend.device)
+        start = time.perf_counter()
+        theta, fit, steps = generation(backend, theta, cfg, hidden, gen)
+        torch.cuda.synchronize(backend.device)
+        train_seconds += time.perf_counter() - start
+        env_steps += int(steps.sum().item())
+        score = evaluate(task, mean_policy(theta, hidden, task), device=backend.device)
+        log(gen, env_steps, train_seconds, float(fit.mean().item()), score)
+        if score >= solved_at:
+            return Result(True, gen, env_steps, train_seconds, score)
+        if train_seconds >= cfg.time_budget:
+            break
+    return Result(False, gen, env_steps, train_seconds, score)
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--task", choices=sorted(TASKS), default="cartpole")
+    p.add_argument("--pop", type=int, default=1024)
+    p.add_argument("--backend", choices=BACKENDS, default="fused")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--lr", type=float, default=0.1)
+    p.add_argument("--sigma", type=float, default=0.1)
+    p.add_argument("--time-budget", type=float, default=120.0)
+    p.add_argument("--max-generations", type=int, default=500)
+    p.add_argument("--assist", type=float, default=0.0)
+    p.add_argument("--start-velocity", type=float, default=0.0)
+    p.add_argument("--anneal", type=int, default=300)
+    a = p.parse_args()
+    cfg = Config(task=a.task, pop=a.pop, lr=a.lr, sigma=a.sigma, time_budget=a.time_budget,
+                 max_generations=a.max_generations, assist_k0=a.assist, start_velocity=a.start_velocity,
+                 anneal_gens=a.anneal)
+    result = train(cfg, a.backend, a.seed, log=lambda gen, es_, secs, fit, score: print(
+        f"gen {gen:4d}  env_steps {es_:>13,}  train {secs:7.2f}s  pop fitness {fit:8.1f}  score {score:8.1f}",
+        flush=True))
+    print(result)
+
+
+if __name__ == "__main__":
+    main()

@@ -60,3 +60,45 @@ def legged_action(logits, c):
     for k in range(c):
         out = out + np.argmax(logits[:, 3 * k:3 * k + 3], axis=-1).astype(np.int32) * 3**k
     return out
+
+
+def steps_fitness(steps_survived, horizon, sign):
+    """(fitness, steps taken) from a fused kernel's steps survived; ``es.py:96-103``:
+    fitness = sign * steps, steps taken = min(steps + 1, horizon)."""
+    steps_survived = np.asarray(steps_survived, dtype=F32)
+    return F32(sign) * steps_survived, np.minimum(steps_survived + 1, horizon)
+
+
+def loop_fitness(step, logits, action_of, state, params, horizon, seed0, alive_bonus=1.0, fall_penalty=0.0,
+                 height_gate=0.0):
+    """Reward sum to the first termination and steps taken, stepping the whole population
+    once per iteration with auto-reset; ``es.py:174-193``.
+
+    ``step(state, action, seed)`` is an oracle env step, ``logits(state, *params)`` the
+    population policy, ``action_of(logits)`` the action rule; step t uses counter seed0 + t.
+    Accumulators are float64, as numpy's ``xp.zeros((P,))`` makes them in the reference."""
+    p = state.shape[1]
+    alive = np.ones(p, dtype=bool)
+    fit = np.zeros(p)
+    steps = np.zeros(p)
+    for t in range(horizon):
+        action = action_of(logits(state, *params))
+        state, reward, done = step(state, action, (seed0 + t) & 0xFFFFFFFF)
+        steps = steps + alive.astype(steps.dtype)
+        fell = alive & done
+        alive = alive & ~done
+        if height_gate:
+            forward = (reward - 1.0) * (state[1] >= height_gate).astype(fit.dtype)
+        else:
+            forward = reward - 1.0
+        fit = fit + (forward + alive_bonus) * alive.astype(fit.dtype) - fall_penalty * fell.astype(fit.dtype)
+    return fit, steps
+
+
+def generation_update(theta, eps, fitness, sigma, lr):
+    """theta + lr * sum(rank * eps) / (P * sigma) with stable centered ranks; ``es.py:218-227``
+    given the noise ``eps`` (P, D) and the population fitness."""
+    p = eps.shape[0]
+    ranks = centered_ranks(np.asarray(fitness, dtype=F32))
+    grad = (ranks[:, None] * eps).sum(axis=0) / (p * sigma)
+    return theta + lr * grad
