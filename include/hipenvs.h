@@ -114,6 +114,44 @@ int hipenvs_acrobot_step(const float* state, const int32_t* action, uint32_t see
 int hipenvs_acrobot_es_rollout(const float* state, const float* theta, int64_t p, int32_t hidden,
                                int32_t horizon, float* steps, hipenvs_stream_t stream);
 
+/* ---- K-link pendulum, articulated-body algorithm ----------------------- */
+/* k (links) in {1, 2, 3, 4, 8, 16, 32, 64}; state (2k, n) f32: absolute angles
+ * then angular velocities. */
+
+/* Fresh states: every row U[+-0.1] (zero_velocity == 0, the RK4 task's reset),
+ * or angles U[+-0.1] and zero velocities (the Euler task's), at counter `seed`;
+ * row p hashed at (seed ^ (i * 0x9E3779B9)) + p * 0x85EBCA6B.
+ * Replaces pendulum_aba_mlx.Pendulum.reset (MLX RNG) used beside
+ * pendulum_aba_metal.py:119-144. */
+int hipenvs_pendulum_aba_reset(int32_t k, int32_t zero_velocity, float* state, int64_t n, uint32_t seed,
+                               hipenvs_stream_t stream);
+
+/* One RK4 step (dt 0.02) of the ABA dynamics, root torque action - 1 for action
+ * (n) i32 in {0, 1, 2}, wrap, clip at 10 pi, terminate when -sum cos th > k/2,
+ * reward -1 (0 on done), masked reset. Replaces the `pendulum{k}_aba_step` Metal
+ * kernel and pendulum_aba_metal.Pendulum.step (pendulum_aba_metal.py:85-144). */
+int hipenvs_pendulum_aba_step(int32_t k, const float* state, const int32_t* action, uint32_t seed,
+                              float* next_state, float* reward, uint8_t* done, int64_t n,
+                              hipenvs_stream_t stream);
+
+/* One semi-implicit Euler step (dt 0.01): omega += dt * acc, theta += dt * omega,
+ * with a continuous root torque torque (n) f32, or, when `torque` is NULL,
+ * U[-1, 1) from pcg_hash((seed ^ (i * 0x9E3779B9)) + 0xD3A2646C). Same wrap,
+ * clip, termination and reward as the RK4 step; resets to angles U[+-0.1] and
+ * zero velocities. No reference kernel: the reference integrates with RK4 only
+ * (pendulum_aba_np.py:117-123); this is the integrator of the K-link benchmark
+ * configuration. */
+int hipenvs_pendulum_aba_step_euler(int32_t k, const float* state, const float* torque, uint32_t seed,
+                                    float* next_state, float* reward, uint8_t* done, int64_t n,
+                                    hipenvs_stream_t stream);
+
+/* Absolute angular accelerations acc (k, n) of state (2k, n) under root torque
+ * (n): the ABA alone. Replaces pendulum_aba_np.aba_accelerations
+ * (pendulum_aba_np.py:30-99) / the `aba<K>` Metal function
+ * (pendulum_aba_metal.py:24-82). */
+int hipenvs_pendulum_aba_accelerations(int32_t k, const float* state, const float* torque, float* acc,
+                                       int64_t n, hipenvs_stream_t stream);
+
 /* ---- Diagnostics (no reference counterpart) ---------------------------- */
 
 /* Elementwise deterministic sin, cos, tanh of x (n) as the kernels compute them;

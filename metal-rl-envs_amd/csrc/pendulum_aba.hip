@@ -1,0 +1,358 @@
+// The K-link planar pendulum by Featherstone's articulated-body algorithm on
+// MI355X: accelerations, the RK4 step of the reference (dt 0.02, discrete root
+// torque) and the semi-implicit Euler step with a continuous root torque
+// (dt 0.01), each one thread per environment with the chain in registers.
+//
+// The three passes follow pendulum_aba_np.py:30-99 operation by operation:
+// outward link velocities; inward articulated inertia Ia = IA - U U^T / D and
+// bias pa = p + Ia c + U u / D folded into the parent through X^T (.) X; outward
+// accelerations with the base accelerating at -g; the running sum turns joint
+// accelerations into absolute ones. Per link the kernel keeps cos/sin of the
+// joint angle, the link velocity and U, u (9 floats); K is a template constant
+// so every per-link array is indexed statically and lives in VGPRs/AGPRs.
+//
+// Algorithmic bytes per env-step: 2K floats in, 2K floats out, 4 B action or
+// torque, 4 B reward, 1 B done = 16K + 9 B.
+
+#include "hipenvs_device.h"
+
+namespace hipenvs {
+namespace aba {
+
+constexpr float GRAVITY = 0x1.39999ap+3f;     // float32(9.8)
+constexpr float DT = 0x1.47ae14p-6f;          // float32(0.02)
+constexpr float DT_2 = 0x1.47ae14p-7f;        // float32(0.02 / 2)
+constexpr float DT_6 = 0x1.b4e81cp-9f;        // float32(0.02 / 6)
+constexpr float DT_EULER = 0x1.47ae14p-7f;    // float32(0.01)
+constexpr float MAX_VEL = 0x1.f6a7a2p+4f;     // float32(10 * pi)
+constexpr float RESET_BOUND = 0x1.99999ap-4f; // float32(0.1)
+constexpr float TWO_PI = 0x1.921fb6p+2f;      // float32(2 * pi)
+constexpr float PI = 0x1.921fb6p+1f;          // float32(pi)
+
+__device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf((x + PI) / TWO_PI); }
+
+// Velocity-product bias p = v x* (I v) of a unit mass at (1, 0) (pendulum_aba_np.py:46-47).
+__device__ __forceinline__ void own_bias(float w, float x, float y, float& p0, float& p1, float& p2) {
+  const float f = w + y;
+  p0 = x * f - y * x;
+  p1 = (-w) * f;
+  p2 = w * x;
+}
+
+// Absolute angular accelerations acc[K] from absolute angles th[K] and velocities om[K].
+template <int K>
+__device__ __forceinline__ void accelerations(const float* th, const float* om, float torque, float* acc) {
+  float cs[K], sn[K], vw[K], vx[K], vy[K], U0[K], U1[K], U2[K], uu[K];
+  // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
+  {
+    float w = 0.0f, x = 0.0f, y = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int im = i > 0 ? i - 1 : 0;
+      const float q = (i == 0) ? th[0] : th[i] - th[im];
+      const float qd = (i == 0) ? om[0] : om[i] - om[im];
+      det_sincos(q, &sn[i], &cs[i]);
+      const float xy = (i == 0) ? (y + w * 0.0f) : (y + w);
+      const float nw = w + qd;
+      const float nx = cs[i] * x + sn[i] * xy;
+      const float ny = (-sn[i]) * x + cs[i] * xy;
+      vw[i] = nw;
+      vx[i] = nx;
+      vy[i] = ny;
+      w = nw;
+      x = nx;
+      y = ny;
+    }
+  }
+  // inward: articulated inertia A and bias P of the current link, folded into the parent
+  // (pendulum_aba_np.py:51-82)
+  {
+    float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
+    float P0, P1, P2;
+    own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
+#pragma unroll
+    for (int i = K - 1; i >= 0; --i) {
+      U0[i] = A0;
+      U1[i] = A1;
+      U2[i] = A2;
+      uu[i] = (i == 0 ? torque : 0.0f) - P0;
+      if (i == 0) break;
+      const float D = A0;
+      const float I0 = A0 - (A0 * A0) / D, I1 = A1 - (A0 * A1) / D, I2 = A2 - (A0 * A2) / D;
+      const float I3 = A3 - (A1 * A1) / D, I4 = A4 - (A1 * A2) / D, I5 = A5 - (A2 * A2) / D;
+      const float qd = om[i] - om[i - 1];
+      const float c1 = qd * vy[i], c2 = (-qd) * vx[i];
+      // Ia c with c = (0, c1, c2); the reference adds the exact zero term Ia_j0 * 0 first.
+      const float Iac0 = I1 * c1 + I2 * c2;
+      const float Iac1 = I3 * c1 + I4 * c2;
+      const float Iac2 = I4 * c1 + I5 * c2;
+      const float g = uu[i] / D;
+      const float pa0 = (P0 + Iac0) + A0 * g;
+      const float pa1 = (P1 + Iac1) + A1 * g;
+      const float pa2 = (P2 + Iac2) + A2 * g;
+      const float c = cs[i], s = sn[i];
+      // B = Ia X, X = [[1, 0, 0], [s, c, s], [c, -s, c]] (joint at (1, 0) in the parent)
+      const float B00 = (I0 + I1 * s) + I2 * c, B01 = I1 * c - I2 * s, B02 = I1 * s + I2 * c;
+      const float B10 = (I1 + I3 * s) + I4 * c, B11 = I3 * c - I4 * s, B12 = I3 * s + I4 * c;
+      const float B20 = (I2 + I4 * s) + I5 * c, B21 = I4 * c - I5 * s, B22 = I4 * s + I5 * c;
+      // parent's own inertia (1, 0, 1, 1, 0, 1) + X^T B
+      A0 = 1.0f + ((B00 + s * B10) + c * B20);
+      A1 = (B01 + s * B11) + c * B21;
+      A2 = 1.0f + ((B02 + s * B12) + c * B22);
+      A3 = 1.0f + (c * B11 - s * B21);
+      A4 = c * B12 - s * B22;
+      A5 = 1.0f + (s * B12 + c * B22);
+      // parent's own bias + X^T pa
+      float pp0, pp1, pp2;
+      own_bias(vw[i - 1], vx[i - 1], vy[i - 1], pp0, pp1, pp2);
+      P0 = ((pp0 + pa0) + s * pa1) + c * pa2;
+      P1 = (pp1 + c * pa1) - s * pa2;
+      P2 = (pp2 + s * pa1) + c * pa2;
+    }
+  }
+  // outward: accelerations from a base accelerating at -g (pendulum_aba_np.py:83-99)
+  {
+    float aw = 0.0f, ax = -GRAVITY, ay = 0.0f, run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int im = i > 0 ? i - 1 : 0;
+      const float c = cs[i], s = sn[i];
+      const float xy = (i == 0) ? (ay + aw * 0.0f) : (ay + aw);
+      const float qd = (i == 0) ? om[0] : om[i] - om[im];
+      const float c1 = qd * vy[i], c2 = (-qd) * vx[i];
+      const float ap0 = aw;
+      const float ap1 = (c * ax + s * xy) + c1;
+      const float ap2 = ((-s) * ax + c * xy) + c2;
+      const float qdd = (uu[i] - ((U0[i] * ap0 + U1[i] * ap1) + U2[i] * ap2)) / U0[i];
+      aw = ap0 + qdd;
+      ax = ap1;
+      ay = ap2;
+      run = run + qdd;
+      acc[i] = run;
+    }
+  }
+}
+
+// Tip above half the chain's length: -(sum_i cos th_i) > K / 2 (pendulum_np.py:81-82).
+template <int K>
+__device__ __forceinline__ bool terminal(const float* th) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < K; ++i) s = (i == 0) ? det_cos(th[0]) : s + det_cos(th[i]);
+  return -s > (float)K * 0.5f;
+}
+
+// RK4 at dt 0.02 in place (pendulum_aba_np.py:117-123), stage sums accumulated in numpy's order.
+template <int K>
+__device__ __forceinline__ void rk4(float* th, float* om, float torque) {
+  float acc[K], t[K], o[K], sth[K], som[K];
+  accelerations<K>(th, om, torque, acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    sth[p] = om[p];
+    som[p] = acc[p];
+    t[p] = th[p] + DT_2 * om[p];
+    o[p] = om[p] + DT_2 * acc[p];
+  }
+  accelerations<K>(t, o, torque, acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    sth[p] = sth[p] + 2.0f * o[p];
+    som[p] = som[p] + 2.0f * acc[p];
+    t[p] = th[p] + DT_2 * o[p];
+    o[p] = om[p] + DT_2 * acc[p];
+  }
+  accelerations<K>(t, o, torque, acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    sth[p] = sth[p] + 2.0f * o[p];
+    som[p] = som[p] + 2.0f * acc[p];
+    t[p] = th[p] + DT * o[p];
+    o[p] = om[p] + DT * acc[p];
+  }
+  accelerations<K>(t, o, torque, acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    th[p] = wrap(th[p] + DT_6 * (sth[p] + o[p]));
+    om[p] = clip(om[p] + DT_6 * (som[p] + acc[p]), -MAX_VEL, MAX_VEL);
+  }
+}
+
+// Semi-implicit Euler at dt 0.01 in place: omega first, then theta with the new omega.
+template <int K>
+__device__ __forceinline__ void euler(float* th, float* om, float torque) {
+  float acc[K];
+  accelerations<K>(th, om, torque, acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    const float om_new = om[p] + DT_EULER * acc[p];
+    const float th_new = th[p] + DT_EULER * om_new;
+    th[p] = wrap(th_new);
+    om[p] = clip(om_new, -MAX_VEL, MAX_VEL);
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void load(const float* __restrict__ state, int64_t n, int64_t e, float* th, float* om) {
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    th[p] = state[p * n + e];
+    om[p] = state[(K + p) * n + e];
+  }
+}
+
+// Masked reset: all 2K rows U[+-0.1] (RK4 task) or angles U[+-0.1] and zero velocities (Euler task),
+// row p of env e hashed at (seed ^ e*golden) + p * 0x85EBCA6B (pendulum_aba_metal.py:109-113).
+template <int K, bool kZeroVelocity>
+__device__ __forceinline__ void store_with_reset(float* __restrict__ next, int64_t n, int64_t e, const float* th,
+                                                 const float* om, bool d, uint32_t seed) {
+  const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    const float fresh = uniform_pm(pcg_hash(h + (uint32_t)p * kRowStride), RESET_BOUND);
+    next[p * n + e] = d ? fresh : th[p];
+  }
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    const float fresh = kZeroVelocity ? 0.0f : uniform_pm(pcg_hash(h + (uint32_t)(K + p) * kRowStride), RESET_BOUND);
+    next[(K + p) * n + e] = d ? fresh : om[p];
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(kBlock) void step_rk4_kernel(const float* __restrict__ state,
+                                                          const int32_t* __restrict__ action, uint32_t seed,
+                                                          float* __restrict__ next, float* __restrict__ reward,
+                                                          uint8_t* __restrict__ done, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float th[K], om[K];
+  load<K>(state, n, e, th, om);
+  rk4<K>(th, om, (float)(action[e] - 1) * 1.0f);
+  const bool d = terminal<K>(th);
+  store_with_reset<K, false>(next, n, e, th, om, d, seed);
+  reward[e] = d ? 0.0f : -1.0f;
+  done[e] = d ? 1 : 0;
+}
+
+template <int K, bool kArrayTorque>
+__global__ __launch_bounds__(kBlock) void step_euler_kernel(const float* __restrict__ state,
+                                                            const float* __restrict__ torque, uint32_t seed,
+                                                            float* __restrict__ next, float* __restrict__ reward,
+                                                            uint8_t* __restrict__ done, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float th[K], om[K];
+  load<K>(state, n, e, th, om);
+  const float tq = kArrayTorque ? torque[e]
+                                : uniform_pm(pcg_hash(env_hash(seed, (uint32_t)e) + kTorqueOffset), 1.0f);
+  euler<K>(th, om, tq);
+  const bool d = terminal<K>(th);
+  store_with_reset<K, true>(next, n, e, th, om, d, seed);
+  reward[e] = d ? 0.0f : -1.0f;
+  done[e] = d ? 1 : 0;
+}
+
+template <int K>
+__global__ __launch_bounds__(kBlock) void accelerations_kernel(const float* __restrict__ state,
+                                                               const float* __restrict__ torque,
+                                                               float* __restrict__ acc_out, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float th[K], om[K], acc[K];
+  load<K>(state, n, e, th, om);
+  accelerations<K>(th, om, torque[e], acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) acc_out[p * n + e] = acc[p];
+}
+
+template <int K, bool kZeroVelocity>
+__global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state, uint32_t seed, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float th[K], om[K];
+  store_with_reset<K, kZeroVelocity>(state, n, e, th, om, true, seed);
+}
+
+enum Op { kRk4, kEulerArray, kEulerRng, kAcc, kReset, kResetZeroVel };
+
+template <int K>
+int launch(Op op, const float* state, const void* in, uint32_t seed, float* out, float* reward, uint8_t* done,
+           int64_t n, hipStream_t s) {
+  const dim3 grid(grid_for(n)), block(kBlock);
+  switch (op) {
+    case kRk4:
+      hipLaunchKernelGGL(step_rk4_kernel<K>, grid, block, 0, s, state, (const int32_t*)in, seed, out, reward, done, n);
+      break;
+    case kEulerArray:
+      hipLaunchKernelGGL((step_euler_kernel<K, true>), grid, block, 0, s, state, (const float*)in, seed, out, reward,
+                         done, n);
+      break;
+    case kEulerRng:
+      hipLaunchKernelGGL((step_euler_kernel<K, false>), grid, block, 0, s, state, (const float*)in, seed, out, reward,
+                         done, n);
+      break;
+    case kAcc:
+      hipLaunchKernelGGL(accelerations_kernel<K>, grid, block, 0, s, state, (const float*)in, out, n);
+      break;
+    case kReset:
+      hipLaunchKernelGGL((reset_kernel<K, false>), grid, block, 0, s, out, seed, n);
+      break;
+    case kResetZeroVel:
+      hipLaunchKernelGGL((reset_kernel<K, true>), grid, block, 0, s, out, seed, n);
+      break;
+  }
+  return launch_status();
+}
+
+int dispatch(int32_t k, Op op, const float* state, const void* in, uint32_t seed, float* out, float* reward,
+             uint8_t* done, int64_t n, hipStream_t s) {
+  switch (k) {
+    case 1: return launch<1>(op, state, in, seed, out, reward, done, n, s);
+    case 2: return launch<2>(op, state, in, seed, out, reward, done, n, s);
+    case 3: return launch<3>(op, state, in, seed, out, reward, done, n, s);
+    case 4: return launch<4>(op, state, in, seed, out, reward, done, n, s);
+    case 8: return launch<8>(op, state, in, seed, out, reward, done, n, s);
+    case 16: return launch<16>(op, state, in, seed, out, reward, done, n, s);
+    case 32: return launch<32>(op, state, in, seed, out, reward, done, n, s);
+    case 64: return launch<64>(op, state, in, seed, out, reward, done, n, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+
+}  // namespace aba
+}  // namespace hipenvs
+
+using namespace hipenvs;
+
+extern "C" int hipenvs_pendulum_aba_reset(int32_t k, int32_t zero_velocity, float* state, int64_t n, uint32_t seed,
+                                          hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && !state)) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  return aba::dispatch(k, zero_velocity ? aba::kResetZeroVel : aba::kReset, nullptr, nullptr, seed, state, nullptr,
+                       nullptr, n, as_stream(stream));
+}
+
+extern "C" int hipenvs_pendulum_aba_step(int32_t k, const float* state, const int32_t* action, uint32_t seed,
+                                         float* next_state, float* reward, uint8_t* done, int64_t n,
+                                         hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !action || !next_state || !reward || !done))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  return aba::dispatch(k, aba::kRk4, state, action, seed, next_state, reward, done, n, as_stream(stream));
+}
+
+extern "C" int hipenvs_pendulum_aba_step_euler(int32_t k, const float* state, const float* torque, uint32_t seed,
+                                               float* next_state, float* reward, uint8_t* done, int64_t n,
+                                               hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !next_state || !reward || !done))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  return aba::dispatch(k, torque ? aba::kEulerArray : aba::kEulerRng, state, torque, seed, next_state, reward, done,
+                       n, as_stream(stream));
+}
+
+extern "C" int hipenvs_pendulum_aba_accelerations(int32_t k, const float* state, const float* torque, float* acc,
+                                                  int64_t n, hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !torque || !acc))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  return aba::dispatch(k, aba::kAcc, state, torque, 0, acc, nullptr, nullptr, n, as_stream(stream));
+}

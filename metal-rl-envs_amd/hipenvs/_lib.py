@@ -35,6 +35,10 @@ SIGNATURES = {
     "hipenvs_acrobot_reset": [_P, _I64, _U32, _P],
     "hipenvs_acrobot_step": [_P, _P, _U32, _P, _P, _P, _I64, _P],
     "hipenvs_acrobot_es_rollout": [_P, _P, _I64, _I32, _I32, _P, _P],
+    "hipenvs_pendulum_aba_reset": [_I32, _I32, _P, _I64, _U32, _P],
+    "hipenvs_pendulum_aba_step": [_I32, _P, _P, _U32, _P, _P, _P, _I64, _P],
+    "hipenvs_pendulum_aba_step_euler": [_I32, _P, _P, _U32, _P, _P, _P, _I64, _P],
+    "hipenvs_pendulum_aba_accelerations": [_I32, _P, _P, _P, _I64, _P],
 }
 
 

@@ -82,3 +82,10 @@ def test_kernel_constants_are_float32_of_the_reference_values():
     for name, value, expr in consts:
         expect = float(np.float32(eval(expr, {"pi": math.pi, "np": np})))
         assert value == expect, (name, expr, value, expect)
+
+
+def test_unsupported_shapes_are_rejected_on_the_host():
+    from hipenvs import pendulum_aba
+
+    with pytest.raises(ValueError):
+        pendulum_aba.Pendulum(5)
