@@ -152,6 +152,42 @@ int hipenvs_pendulum_aba_step_euler(int32_t k, const float* state, const float* 
 int hipenvs_pendulum_aba_accelerations(int32_t k, const float* state, const float* torque, float* acc,
                                        int64_t n, hipenvs_stream_t stream);
 
+/* ---- C-legged body with hard contacts ---------------------------------- */
+/* state (2(3+c), n) f32: q = (x, y, phi, psi_1..psi_c), then the velocities.
+ * `stand` is the standing pose (2(3+c)) f32 (legged_np.stand_pose). */
+
+/* Fresh states stand + U[+-0.05] at counter `seed`, row j hashed at
+ * (seed ^ (i * 0x9E3779B9)) + j * 0x85EBCA6B; c in {1, 2, 3, 4}.
+ * Replaces legged_mlx.Legged.reset (legged_mlx.py:21-22). */
+int hipenvs_legged_reset(int32_t c, const float* stand, float* state, int64_t n, uint32_t seed,
+                         hipenvs_stream_t stream);
+
+/* One control step: four semi-implicit Euler substeps of 0.01 s, each with a
+ * dense Cholesky of the (3+c)^2 mass matrix and `iters` (0..4096) sweeps of
+ * block projected Gauss-Seidel over the c contacts; action (n) i32 in
+ * [0, 3^c); `assist` is the torso spring-damper stiffness (the stiffness and
+ * 0.1 * assist are rounded to f32 from the double, as numpy does). Reward
+ * forward velocity + 1, 0 on a fall (y < 0.6 or |phi| > 1); masked reset.
+ * Replaces the `legged{c}_step` Metal kernel and legged_metal.Legged.step
+ * (legged_metal.py:13-185). */
+int hipenvs_legged_step(int32_t c, int32_t iters, double assist, const float* state, const int32_t* action,
+                        uint32_t seed, const float* stand, float* next_state, float* reward, uint8_t* done,
+                        int64_t n, hipenvs_stream_t stream);
+
+/* Fused ES rollout on the legged body: one thread per member runs its
+ * (5+2c)-H-3c tanh policy (one three-way head per leg) and the physics for up
+ * to `horizon` steps; fitness (p) = sum of ((v_x if y >= height_gate else 0) +
+ * alive_bonus) until the first fall, minus fall_penalty at it; steps (p) = steps
+ * taken including the falling one. layout 0: theta (p, D) rows in es.unflatten's
+ * layout; layout 1: theta (D, p) columns. c in {1, 2, 4}, hidden in
+ * {4, 8, 16, 32, 64}, iters 0..4096.
+ * Replaces the `legged_es_rollout` Metal kernel and legged_rollout_metal.rollout
+ * (legged_rollout_metal.py:19-83), whose ITERS the reference fixes at 8. */
+int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iters, int32_t layout, const float* state,
+                              const float* theta, int64_t p, int32_t horizon, float alive_bonus,
+                              float fall_penalty, float height_gate, double assist, float* fitness, float* steps,
+                              hipenvs_stream_t stream);
+
 /* ---- Diagnostics (no reference counterpart) ---------------------------- */
 
 /* Elementwise deterministic sin, cos, tanh of x (n) as the kernels compute them;

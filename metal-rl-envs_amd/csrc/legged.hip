@@ -1,0 +1,424 @@
+// The C-legged body with hard ground contacts on MI355X: the env step and the
+// fused legged ES rollout, one thread per environment, everything in VGPRs.
+//
+// Physics: legged_np.py:57-97 in float32, operation by operation. Per substep:
+// foot Jacobians (C sincos), the (3+C)^2 mass matrix, a dense Cholesky reused
+// for the free velocity and the 2C columns M^-1 J^T, the C^2 Delassus blocks,
+// `iters` sweeps of block projected Gauss-Seidel with the exact single-contact
+// solve (hopper_np.py:80-109), semi-implicit Euler. Terms the reference
+// multiplies by an exact zero or one are elided where that leaves every value
+// unchanged (x * 1 = x, x + (+-0) = x); the order of every remaining operation
+// is numpy's.
+//
+// The rollout runs each member's (5+2C)-H-3C tanh policy (one three-way head
+// per leg) and the physics for the whole horizon (legged_rollout_metal.py:19-59).
+// The member's weights are streamed from memory every step (D = 1,676 floats at
+// C = 4, H = 64 do not fit in registers), either from es.unflatten's rows
+// (P, D) or from a column layout (D, P) in which a wave's 64 members read 256
+// contiguous bytes per weight.
+
+#include "hipenvs_device.h"
+
+namespace hipenvs {
+namespace lg {
+
+constexpr float M_F = 0x1.99999ap-3f;              // float32(0.2)
+constexpr float I_T = 0x1.99999ap-4f;              // float32(0.1)
+constexpr float GRAVITY = 0x1.39999ap+3f;          // float32(9.8)
+constexpr float NEG_M_F = -0x1.99999ap-3f;         // float32(-0.2)
+constexpr float H = 0x1.47ae14p-7f;                // float32(0.01)
+constexpr float MU = 0x1.666666p-1f;               // float32(0.7)
+constexpr float BAUMGARTE_OVER_H = 0x1.4p+4f;      // float32(0.2 / 0.01)
+constexpr float FALL_HEIGHT = 0x1.333334p-1f;      // float32(0.6)
+constexpr float FALL_ANGLE = 0x1p+0f;              // float32(1.0)
+constexpr float RESET_BOUND = 0x1.99999ap-5f;      // float32(0.05)
+constexpr float TORQUE = 0x1p+1f;                  // float32(2.0)
+constexpr int SUBSTEPS = 4;
+
+// np.maximum(x, 0.0): NaN propagates.
+__device__ __forceinline__ float max0(float x) { return (x < 0.0f) ? 0.0f : x; }
+
+// Exact impulse of one contact given its Delassus block and relative velocity
+// (hopper_np.py:80-109), float32 throughout.
+__device__ __forceinline__ void contact_impulse(float Att, float Atn, float Ann, float wt, float wn, float depth,
+                                                float& lt_out, float& ln_out) {
+  const bool touching = depth >= 0.0f;
+  const float target = BAUMGARTE_OVER_H * max0(depth);
+  const float det = Att * Ann - Atn * Atn;
+  const float tw = target - wn;
+  const float ln_stick = (Att * tw + Atn * wt) / det;
+  const float lt_stick = ((-Ann) * wt - Atn * tw) / det;
+  const bool sticks = fabsf(lt_stick) <= MU * ln_stick;
+  const float den_p = Ann + MU * Atn, den_m = Ann - MU * Atn;
+  const float ln_p = (den_p > 0.0f) ? max0(tw / den_p) : 0.0f;
+  const float ln_m = (den_m > 0.0f) ? max0(tw / den_m) : 0.0f;
+  const float slip_p = wt + (Att * MU + Atn) * ln_p;
+  const float s = (slip_p <= 0.0f) ? 1.0f : -1.0f;
+  const float ln_slide = (slip_p <= 0.0f) ? ln_p : ln_m;
+  const float lt_slide = (MU * s) * ln_slide;
+  const float ln = sticks ? ln_stick : ln_slide;
+  const float lt = sticks ? lt_stick : lt_slide;
+  const bool active = touching && (ln > 0.0f) && (wn < target);
+  lt_out = active ? lt : 0.0f;
+  ln_out = active ? ln : 0.0f;
+}
+
+// Solve L L^T x = b in place (pendulum_np.py:95-107): forward then backward substitution.
+template <int N>
+__device__ __forceinline__ void chol_solve(const float (&L)[N][N], float (&b)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float s = b[i];
+#pragma unroll
+    for (int p = 0; p < i; ++p) s = s - L[i][p] * b[p];
+    b[i] = s / L[i][i];
+  }
+#pragma unroll
+  for (int i = N - 1; i >= 0; --i) {
+    float s = b[i];
+#pragma unroll
+    for (int p = i + 1; p < N; ++p) s = s - L[p][i] * b[p];
+    b[i] = s / L[i][i];
+  }
+}
+
+// One semi-implicit Euler substep with block PGS contacts, in place (legged_np.py:57-97).
+template <int C>
+__device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
+                                        float assist, float assist_damping) {
+  constexpr int N = 3 + C;
+  float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    const float a = q[2] + q[3 + k];
+    det_sincos(a, &sa[k], &ca[k]);
+    const float ad = v[2] + v[3 + k];
+    dx[k] = ((-sa[k]) * ad) * ad;
+    dy[k] = (ca[k] * ad) * ad;
+    depth[k] = -(q[1] - ca[k]);
+    r2[k] = ca[k] * ca[k] + sa[k] * sa[k];
+  }
+  // sums over the feet in the reference's order
+  float s_ca = ca[0], s_sa = sa[0], s_r2 = r2[0], s_dx = dx[0], s_dy = dy[0], s_f2 = ca[0] * dx[0] + sa[0] * dy[0];
+#pragma unroll
+  for (int k = 1; k < C; ++k) {
+    s_ca = s_ca + ca[k];
+    s_sa = s_sa + sa[k];
+    s_r2 = s_r2 + r2[k];
+    s_dx = s_dx + dx[k];
+    s_dy = s_dy + dy[k];
+    s_f2 = s_f2 + (ca[k] * dx[k] + sa[k] * dy[k]);
+  }
+  // mass matrix, lower triangle (M_T = 1: base 1 + M_F * C on x and y)
+  float L[N][N];
+  const float mxy = 1.0f + M_F * (float)C;
+  L[0][0] = mxy;
+  L[1][0] = M_F * 0.0f;
+  L[1][1] = mxy;
+  L[2][0] = M_F * s_ca;
+  L[2][1] = M_F * s_sa;
+  L[2][2] = I_T + M_F * s_r2;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    L[3 + j][0] = M_F * ca[j];
+    L[3 + j][1] = M_F * sa[j];
+    L[3 + j][2] = M_F * r2[j];
+#pragma unroll
+    for (int i = 0; i < j; ++i) L[3 + j][3 + i] = M_F * 0.0f;
+    L[3 + j][3 + j] = M_F * r2[j];
+  }
+  // generalised forces: bias, gravity, leg torques, torso assist
+  float f[N];
+  f[0] = NEG_M_F * s_dx;
+  f[1] = NEG_M_F * s_dy - GRAVITY * (M_F * (float)C + 1.0f);
+  f[2] = NEG_M_F * s_f2 - GRAVITY * (M_F * s_sa);
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    f[3 + j] = NEG_M_F * (ca[j] * dx[j] + sa[j] * dy[j]) - GRAVITY * (M_F * sa[j]);
+    f[3 + j] = f[3 + j] + tq[j];
+  }
+  f[2] = (f[2] - assist * q[2]) - assist_damping * v[2];
+  // Cholesky in place (pendulum_np.py:88-94)
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+#pragma unroll
+    for (int j = 0; j <= i; ++j) {
+      float s = L[i][j];
+#pragma unroll
+      for (int p = 0; p < j; ++p) s = s - L[i][p] * L[j][p];
+      L[i][j] = (i == j) ? sqrtf(s) : s / L[j][j];
+    }
+  }
+  chol_solve<N>(L, f);
+  float vf[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) vf[i] = v[i] + H * f[i];
+  // M^-1 J^T columns
+  float MiJt[C][N], MiJn[C][N];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      MiJt[k][i] = (i == 0) ? 1.0f : (i == 2 || i == 3 + k) ? ca[k] : 0.0f;
+      MiJn[k][i] = (i == 1) ? 1.0f : (i == 2 || i == 3 + k) ? sa[k] : 0.0f;
+    }
+    chol_solve<N>(L, MiJt[k]);
+    chol_solve<N>(L, MiJn[k]);
+  }
+  // Delassus blocks A[k][l] = (Jt_k.MiJt_l, Jt_k.MiJn_l, Jn_k.MiJt_l, Jn_k.MiJn_l) and free velocities
+  float Att[C][C], Atn[C][C], Ant[C][C], Ann[C][C], w0t[C], w0n[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+#pragma unroll
+    for (int l = 0; l < C; ++l) {
+      Att[k][l] = (MiJt[l][0] + ca[k] * MiJt[l][2]) + ca[k] * MiJt[l][3 + k];
+      Atn[k][l] = (MiJn[l][0] + ca[k] * MiJn[l][2]) + ca[k] * MiJn[l][3 + k];
+      Ant[k][l] = (MiJt[l][1] + sa[k] * MiJt[l][2]) + sa[k] * MiJt[l][3 + k];
+      Ann[k][l] = (MiJn[l][1] + sa[k] * MiJn[l][2]) + sa[k] * MiJn[l][3 + k];
+    }
+    w0t[k] = (vf[0] + ca[k] * vf[2]) + ca[k] * vf[3 + k];
+    w0n[k] = (vf[1] + sa[k] * vf[2]) + sa[k] * vf[3 + k];
+  }
+  // block projected Gauss-Seidel, fixed contact order (legged_np.py:88-93)
+  float lt[C], ln[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    lt[k] = 0.0f;
+    ln[k] = 0.0f;
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      float st = 0.0f, sn = 0.0f;
+      bool first = true;
+#pragma unroll
+      for (int l = 0; l < C; ++l) {
+        if (l == k) continue;
+        const float tt = Att[k][l] * lt[l] + Atn[k][l] * ln[l];
+        const float nn = Ant[k][l] * lt[l] + Ann[k][l] * ln[l];
+        st = first ? tt : st + tt;
+        sn = first ? nn : sn + nn;
+        first = false;
+      }
+      const float wt = (C == 1) ? w0t[k] : w0t[k] + st;
+      const float wn = (C == 1) ? w0n[k] : w0n[k] + sn;
+      contact_impulse(Att[k][k], Atn[k][k], Ann[k][k], wt, wn, depth[k], lt[k], ln[k]);
+    }
+  }
+  // v = v_free + sum_k M^-1 J_k^T lambda_k; q += h v
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float s = MiJt[0][i] * lt[0] + MiJn[0][i] * ln[0];
+#pragma unroll
+    for (int k = 1; k < C; ++k) s = s + (MiJt[k][i] * lt[k] + MiJn[k][i] * ln[k]);
+    const float vn = vf[i] + s;
+    v[i] = vn;
+    q[i] = q[i] + H * vn;
+  }
+}
+
+template <int C>
+__device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
+  return (q[1] < FALL_HEIGHT) || (fabsf(q[2]) > FALL_ANGLE);
+}
+
+template <int C>
+__global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ state,
+                                                      const int32_t* __restrict__ action, uint32_t seed,
+                                                      const float* __restrict__ stand, int iters, float assist,
+                                                      float assist_damping, float* __restrict__ next,
+                                                      float* __restrict__ reward, uint8_t* __restrict__ done,
+                                                      int64_t n) {
+  constexpr int N = 3 + C;
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float q[N], v[N], tq[C];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = state[i * n + e];
+    v[i] = state[(N + i) * n + e];
+  }
+  // leg k gets ((a / 3^k) % 3 - 1) * TORQUE (legged_np.py:51-54)
+  int32_t a = action[e];
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    tq[k] = (float)(a % 3 - 1) * TORQUE;
+    a /= 3;
+  }
+#pragma unroll 1
+  for (int s = 0; s < SUBSTEPS; ++s) substep<C>(q, v, tq, iters, assist, assist_damping);
+  const bool d = fallen<C>(q);
+  const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+  for (int i = 0; i < 2 * N; ++i) {
+    const float fresh = stand[i] + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
+    next[i * n + e] = d ? fresh : (i < N ? q[i] : v[i - N]);
+  }
+  reward[e] = d ? 0.0f : v[0] + 1.0f;
+  done[e] = d ? 1 : 0;
+}
+
+template <int C>
+__global__ __launch_bounds__(kBlock) void reset_kernel(const float* __restrict__ stand, float* __restrict__ state,
+                                                       uint32_t seed, int64_t n) {
+  constexpr int N = 3 + C;
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+  for (int i = 0; i < 2 * N; ++i)
+    state[i * n + e] = stand[i] + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
+}
+
+// Fused ES rollout (legged_rollout_metal.py:19-59). Weight d of member i is
+// theta[i * D + d] (rows) or theta[d * p + i] (columns).
+template <int C, int HID, bool kColumns>
+__global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
+                                                     int64_t p, int32_t horizon, int iters, float alive, float fall,
+                                                     float gate, float assist, float assist_damping,
+                                                     float* __restrict__ fitness, float* __restrict__ steps_out) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  constexpr int B1 = OBS * HID, W2 = B1 + HID, B2 = W2 + HID * OUT;
+  const int64_t e = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (e >= p) return;
+  const float* w = kColumns ? theta + e : theta + e * D;
+  const int64_t stride = kColumns ? p : 1;
+  float q[N], v[N], tq[C];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = state[i * p + e];
+    v[i] = state[(N + i) * p + e];
+  }
+  float total = 0.0f, taken = 0.0f;
+  for (int32_t t = 0; t < horizon; ++t) {
+    float obs[OBS];
+#pragma unroll
+    for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
+    float logit[OUT];
+#pragma unroll
+    for (int o = 0; o < OUT; ++o) logit[o] = w[(B2 + o) * stride];
+#pragma unroll 2
+    for (int j = 0; j < HID; ++j) {
+      float s = w[(B1 + j) * stride];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) s = s + obs[k] * w[(k * HID + j) * stride];
+      const float hj = det_tanh(s);
+#pragma unroll
+      for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w[(W2 + j * OUT + o) * stride];
+    }
+#pragma unroll
+    for (int leg = 0; leg < C; ++leg) {
+      float torque = -1.0f, best = logit[3 * leg];
+      if (logit[3 * leg + 1] > best) { torque = 0.0f; best = logit[3 * leg + 1]; }
+      if (logit[3 * leg + 2] > best) { torque = 1.0f; }
+      tq[leg] = torque * TORQUE;
+    }
+#pragma unroll 1
+    for (int s = 0; s < SUBSTEPS; ++s) substep<C>(q, v, tq, iters, assist, assist_damping);
+    if (fallen<C>(q)) {
+      taken += 1.0f;
+      total = total - fall;
+      break;
+    }
+    total = total + (((q[1] >= gate) ? v[0] : 0.0f) + alive);
+    taken += 1.0f;
+  }
+  fitness[e] = total;
+  steps_out[e] = taken;
+}
+
+template <int C>
+int launch_step(const float* state, const int32_t* action, uint32_t seed, const float* stand, int iters, double assist,
+                float* next, float* reward, uint8_t* done, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL(step_kernel<C>, dim3(grid_for(n)), dim3(kBlock), 0, s, state, action, seed, stand, iters,
+                     (float)assist, (float)(0.1 * assist), next, reward, done, n);
+  return launch_status();
+}
+
+template <int C, int HID>
+int launch_rollout(bool columns, const float* state, const float* theta, int64_t p, int32_t horizon, int iters,
+                   float alive, float fall, float gate, double assist, float* fitness, float* steps, hipStream_t s) {
+  const dim3 grid(grid_for(p, 64)), block(64);
+  if (columns)
+    hipLaunchKernelGGL((rollout_kernel<C, HID, true>), grid, block, 0, s, state, theta, p, horizon, iters, alive, fall,
+                       gate, (float)assist, (float)(0.1 * assist), fitness, steps);
+  else
+    hipLaunchKernelGGL((rollout_kernel<C, HID, false>), grid, block, 0, s, state, theta, p, horizon, iters, alive,
+                       fall, gate, (float)assist, (float)(0.1 * assist), fitness, steps);
+  return launch_status();
+}
+
+template <int C>
+int dispatch_hidden(int32_t hidden, bool columns, const float* state, const float* theta, int64_t p, int32_t horizon,
+                    int iters, float alive, float fall, float gate, double assist, float* fitness, float* steps,
+                    hipStream_t s) {
+  switch (hidden) {
+    case 4: return launch_rollout<C, 4>(columns, state, theta, p, horizon, iters, alive, fall, gate, assist, fitness, steps, s);
+    case 8: return launch_rollout<C, 8>(columns, state, theta, p, horizon, iters, alive, fall, gate, assist, fitness, steps, s);
+    case 16: return launch_rollout<C, 16>(columns, state, theta, p, horizon, iters, alive, fall, gate, assist, fitness, steps, s);
+    case 32: return launch_rollout<C, 32>(columns, state, theta, p, horizon, iters, alive, fall, gate, assist, fitness, steps, s);
+    case 64: return launch_rollout<C, 64>(columns, state, theta, p, horizon, iters, alive, fall, gate, assist, fitness, steps, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+
+}  // namespace lg
+}  // namespace hipenvs
+
+using namespace hipenvs;
+
+static constexpr int kMaxIters = 4096;
+
+extern "C" int hipenvs_legged_reset(int32_t c, const float* stand, float* state, int64_t n, uint32_t seed,
+                                    hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!stand || !state))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid(grid_for(n)), block(kBlock);
+  switch (c) {
+    case 1: hipLaunchKernelGGL(lg::reset_kernel<1>, grid, block, 0, s, stand, state, seed, n); break;
+    case 2: hipLaunchKernelGGL(lg::reset_kernel<2>, grid, block, 0, s, stand, state, seed, n); break;
+    case 3: hipLaunchKernelGGL(lg::reset_kernel<3>, grid, block, 0, s, stand, state, seed, n); break;
+    case 4: hipLaunchKernelGGL(lg::reset_kernel<4>, grid, block, 0, s, stand, state, seed, n); break;
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+extern "C" int hipenvs_legged_step(int32_t c, int32_t iters, double assist, const float* state, const int32_t* action,
+                                   uint32_t seed, const float* stand, float* next_state, float* reward, uint8_t* done,
+                                   int64_t n, hipenvs_stream_t stream) {
+  if (n < 0 || iters < 0 || iters > kMaxIters ||
+      (n > 0 && (!state || !action || !stand || !next_state || !reward || !done)))
+    return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  switch (c) {
+    case 1: return lg::launch_step<1>(state, action, seed, stand, iters, assist, next_state, reward, done, n, s);
+    case 2: return lg::launch_step<2>(state, action, seed, stand, iters, assist, next_state, reward, done, n, s);
+    case 3: return lg::launch_step<3>(state, action, seed, stand, iters, assist, next_state, reward, done, n, s);
+    case 4: return lg::launch_step<4>(state, action, seed, stand, iters, assist, next_state, reward, done, n, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+
+extern "C" int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iters, int32_t layout, const float* state,
+                                         const float* theta, int64_t p, int32_t horizon, float alive_bonus,
+                                         float fall_penalty, float height_gate, double assist, float* fitness,
+                                         float* steps, hipenvs_stream_t stream) {
+  if (p < 0 || horizon < 0 || iters < 0 || iters > kMaxIters || (layout != 0 && layout != 1) ||
+      (p > 0 && (!state || !theta || !fitness || !steps)))
+    return HIPENVS_E_ARG;
+  if (p == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  const bool columns = layout == 1;
+  switch (c) {
+    case 1: return lg::dispatch_hidden<1>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
+    case 2: return lg::dispatch_hidden<2>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
+    case 4: return lg::dispatch_hidden<4>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}

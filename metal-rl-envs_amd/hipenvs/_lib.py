@@ -39,6 +39,10 @@ SIGNATURES = {
     "hipenvs_pendulum_aba_step": [_I32, _P, _P, _U32, _P, _P, _P, _I64, _P],
     "hipenvs_pendulum_aba_step_euler": [_I32, _P, _P, _U32, _P, _P, _P, _I64, _P],
     "hipenvs_pendulum_aba_accelerations": [_I32, _P, _P, _P, _I64, _P],
+    "hipenvs_legged_reset": [_I32, _P, _P, _I64, _U32, _P],
+    "hipenvs_legged_step": [_I32, _I32, ctypes.c_double, _P, _P, _U32, _P, _P, _P, _P, _I64, _P],
+    "hipenvs_legged_es_rollout": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32, ctypes.c_double,
+                                  _P, _P, _P],
 }
 
 

@@ -30,7 +30,7 @@ from typing import Any, Callable
 
 import torch
 
-from . import acrobot, acrobot_rollout, cartpole, cartpole_rollout
+from . import acrobot, acrobot_rollout, cartpole, cartpole_rollout, legged, legged_rollout
 
 
 @dataclass(frozen=True)
@@ -95,6 +95,25 @@ TASKS = {
     "acrobot": Task("acrobot", 6, 3, 32, -100.0, acrobot, acrobot_obs, argmax_action,
                     steps_fitness(acrobot_rollout.rollout_steps, -1.0)),
 }
+
+
+def legged_task(c, name, alive=1.0, fall=0.0, gate=0.0, hidden=16, iters=legged.ITERS):
+    """``es.py:106-114``: training fitness forward velocity (above the gate) + `alive` per step,
+    minus `fall` at a fall; canonical score forward distance until the first fall (threshold 100)."""
+    env = legged.Legged(c, iters)
+
+    def rollout(state, theta_pop, hidden_, horizon, assist=0.0):
+        return legged_rollout.rollout(state, theta_pop, hidden_, horizon, c, alive, fall, gate, assist, iters)
+
+    return Task(f"legged{c}{name}", 5 + 2 * c, 3 * c, hidden, 100.0, env, legged_obs, legged_action(c), rollout,
+                alive, fall, 0.0, gate, 3 + c, True)
+
+
+for _c, _name, _kw in ((2, "", {}), (4, "", {}), (2, "_distance", {"alive": 0.0}), (4, "_distance", {"alive": 0.0}),
+                       (2, "_alive10", {"alive": 0.1}), (2, "_fall", {"alive": 0.0, "fall": 20.0}),
+                       (2, "_alive10_fall", {"alive": 0.1, "fall": 20.0}), (4, "_alive10", {"alive": 0.1}),
+                       (2, "_gated", {"alive": 0.0, "gate": 0.85})):
+    TASKS[f"legged{_c}{_name}"] = legged_task(_c, _name, **_kw)
 
 
 def register(task):

@@ -1,0 +1,138 @@
+"""Legged step and fused legged ES rollout kernels vs the oracle, through the C ABI (GPU).
+
+Bar: bit-exact against the oracle's float32 restatement of legged_np (the
+arithmetic of the reference's Metal kernel). The literal reference promotes to
+float64 inside contact_impulse; the oracle tests bound that gap separately.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import es as oes
+from oracle import legged as olg
+from oracle import rng
+from test_oracle_legged import legged_states
+
+pytestmark = pytest.mark.gpu
+
+
+def to_np(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("c", [1, 2, 3, 4])
+@pytest.mark.parametrize("iters", [1, 8])
+def test_step_matches_oracle(dev, c, iters):
+    from hipenvs import legged
+
+    state, action = legged_states(c, 300, seed=c)
+    body = legged.Legged(c, iters)
+    body.reseed(3)
+    ns, rew, done = body.step(torch.from_numpy(state).to(dev), torch.from_numpy(action.astype(np.int32)).to(dev))
+    ens, erew, edone = olg.Legged(c, iters).step(state, action, seed=4)
+    np.testing.assert_array_equal(to_np(ns), ens)
+    np.testing.assert_array_equal(to_np(rew), erew)
+    np.testing.assert_array_equal(to_np(done), edone)
+
+
+@pytest.mark.parametrize("c", [2, 4])
+def test_step_with_assist_matches_oracle(dev, c):
+    from hipenvs import legged
+
+    state, action = legged_states(c, 200, seed=10 + c)
+    body = legged.Legged(c)
+    body.reseed(0)
+    ns, rew, done = body.step(torch.from_numpy(state).to(dev), torch.from_numpy(action.astype(np.int32)).to(dev), 20.0)
+    ens, erew, edone = olg.Legged(c).step(state, action, seed=1, assist=20.0)
+    np.testing.assert_array_equal(to_np(ns), ens)
+    np.testing.assert_array_equal(to_np(done), edone)
+
+
+@pytest.mark.parametrize("c", [2, 4])
+def test_free_running_chain_identical_flags(dev, c):
+    """Reset, then 40 steps of uniform random actions: identical flags every step."""
+    from hipenvs import legged
+
+    n = 512
+    body, ref = legged.Legged(c), olg.Legged(c)
+    s_dev = body.reset(n, seed=1, device=dev)
+    s_ref = ref.reset(n, seed=1)
+    np.testing.assert_array_equal(to_np(s_dev), s_ref)
+    body.reseed(100)
+    for t in range(101, 141):
+        a = rng.uniform_actions(t, n, 3**c)
+        s_dev, _, d_dev = body.step(s_dev, torch.from_numpy(a).to(dev))
+        s_ref, _, d_ref = ref.step(s_ref, a, seed=t)
+        np.testing.assert_array_equal(to_np(d_dev), d_ref, err_msg=f"step {t}")
+    np.testing.assert_array_equal(to_np(s_dev), s_ref)
+
+
+def _population(p, c, hidden, scale, seed):
+    from hipenvs import legged_rollout
+
+    r = np.random.default_rng(seed)
+    return (r.standard_normal((p, legged_rollout.n_params(hidden, c))) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("c,hidden,p,horizon", [(1, 8, 128, 60), (2, 16, 256, 100), (4, 64, 96, 40)])
+def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon):
+    from hipenvs import legged, legged_rollout
+
+    theta = _population(p, c, hidden, 0.3, c)
+    state = olg.Legged(c).reset(p, seed=7)
+    st, th = torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev)
+    fk, sk = legged_rollout.rollout(st, th, hidden, horizon, c)
+    ef, es_ = olg.rollout_fused(state, theta, hidden, horizon, c)
+    np.testing.assert_array_equal(to_np(fk), ef)
+    np.testing.assert_array_equal(to_np(sk), es_)
+    fc, sc = legged_rollout.rollout(st, th.T.contiguous(), hidden, horizon, c, layout="columns")
+    np.testing.assert_array_equal(to_np(fc), ef)
+    np.testing.assert_array_equal(to_np(sc), es_)
+    assert 1 <= es_.mean() <= horizon
+
+
+def test_shaped_reward_and_assist_match_oracle(dev):
+    """test_es.py:71-104's variants: alive 0.1 + fall penalty 20 (some fitness negative),
+    and the assist spring with a gate."""
+    from hipenvs import legged_rollout
+
+    c, hidden, p, horizon = 2, 16, 256, 80
+    theta = _population(p, c, hidden, 0.3, 11)
+    state = olg.Legged(c).reset(p, seed=2)
+    st, th = torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev)
+    fk, sk = legged_rollout.rollout(st, th, hidden, horizon, c, alive_bonus=0.1, fall_penalty=20.0)
+    ef, es_ = olg.rollout_fused(state, theta, hidden, horizon, c, alive_bonus=0.1, fall_penalty=20.0)
+    np.testing.assert_array_equal(to_np(fk), ef)
+    np.testing.assert_array_equal(to_np(sk), es_)
+    assert (ef < 0).any()
+    fa, sa = legged_rollout.rollout(st, th, hidden, horizon, c, alive_bonus=0.0, height_gate=0.85, assist=20.0)
+    efa, esa = olg.rollout_fused(state, theta, hidden, horizon, c, alive_bonus=0.0, height_gate=0.85, assist=20.0)
+    np.testing.assert_array_equal(to_np(fa), efa)
+    np.testing.assert_array_equal(to_np(sa), esa)
+    assert esa.mean() > 1.5 * es_.mean() or esa.mean() > 0.9 * horizon
+
+
+def test_fused_rollout_close_to_the_oracle_loop(dev):
+    """test_es.py:60-69 for the legged body: the fused kernel against es.loop_fitness over the
+    step (reward - 1 in float32, auto-reset), within the reference's tolerance."""
+    from hipenvs import legged_rollout
+
+    c, hidden, p, horizon = 2, 16, 256, 60
+    theta = _population(p, c, hidden, 0.3, 5)
+    state = olg.Legged(c).reset(p, seed=5)
+    fk, sk = legged_rollout.rollout(torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev), hidden, horizon, c)
+    params = oes.unflatten(theta, hidden, 5 + 2 * c, 3 * c)
+    body = olg.Legged(c)
+
+    def logits(s, *prm):
+        return olg.policy_logits(s[:3 + c], s[3 + c:], *prm, c)
+
+    def action_of(lg_):
+        return oes.legged_action(lg_.T, c)
+
+    fl, sl = oes.loop_fitness(body.step, logits, action_of, state, params, horizon, seed0=1)
+    fk, sk = to_np(fk), to_np(sk)
+    close = np.abs(fk - fl) <= 1e-3 * np.maximum(np.abs(fl), 1.0) + 1e-2
+    assert close.mean() > 0.95 and (sk == sl).mean() > 0.95, (close.mean(), (sk == sl).mean())
+    assert 5 < sl.mean() < 200
