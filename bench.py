@@ -1,29 +1,42 @@
-"""Benchmark of the hipenvs hot path on one MI355X; prints ONE JSON line.
+"""Benchmark of the hipenvs hot path on one MI355X; prints ONE JSON line on stdout
+(progress goes to stderr).
 
-Headline workload: the batched CartPole step at N = 2**18 environments, the
-reference's step kernel API (one launch per env step, cartpole_metal.step),
-over `--steps` steps (default 1,000) after `--warmup` untimed steps. The launches
-of the timed steps are captured once into a HIP graph (outside the clock) and
-replayed, so the clock measures the kernels, not Python. Inputs (state, the
-pre-drawn Bernoulli(0.5) actions of every step) are resident in HBM before the
-clock starts; every step's reward and done rows are written to a (steps, N)
-rollout buffer, as the reference's harness materialises them (bench.py:48-61).
+Headline (`value`): the batched CartPole step at N = 2**18 environments with the
+reference's step-kernel API (one launch per env step, cartpole_metal.step),
+`--steps` timed steps (default 1,000) after `--warmup` untimed ones. The timed
+launches are captured once into a HIP graph outside the clock and replayed, so
+the clock measures the kernels, not Python. Inputs (state and the pre-drawn
+Bernoulli(0.5) actions of every step) are resident in HBM before the clock
+starts; every step's reward and done rows are written to a (steps, N) rollout
+buffer, as the reference's harness materialises them (bench.py:48-61).
 
 Timing rule (the reference's, bench.py:75-82 / README:135-172): env-steps/s =
 N x timed steps / wall seconds, device synchronised before and after the timed
 region, median of `--repeats` repeats.
 
-Roofline: `achieved` = 41 algorithmic bytes per env-step x N / the average
-launch duration, which is the HIP-event time of the timed replay (events on the
-replay's stream) divided by the launches in it. Also measured in the same run
-and reported under "extra": the K = 32 fused kernel (in-kernel and array
-actions).
+`roofline` (cartpole_step): achieved = 41 algorithmic bytes per env-step (16 B
+state in, 4 B action, 16 B state out, 4 B reward, 1 B done) x N / the average
+launch duration, which is the HIP-event time of the timed replay (events on
+the replay's stream) divided by its launches; peak 8 TB/s HBM.
 
-`cpu_baseline`: the CPU oracle's numpy CartPole step (the reference's
-algorithm, np.sin/np.cos, single process) on the same N for a bounded sample
-of about `--cpu-seconds` seconds on this host.
+`cpu_baseline`: the CPU oracle's numpy CartPole step (the reference's algorithm
+and op order with np.sin/np.cos, one process) at the same N for a bounded
+sample of about `--cpu-seconds` seconds on this host.
 
-Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--sweep]
+`extra` holds the rest of the workload list, measured in the same run:
+* `legged4_es_rollout`: the fused legged ES rollout at N = 262,144 members,
+  C = 4 legs, H = 64, sigma 0.03 antithetic around theta0 = 0.1 N(0, 1), alive
+  bonus 1 + forward velocity, horizon 1,000, S = 4/8/16 Gauss-Seidel sweeps:
+  compacting chunked schedule, env-steps (steps taken) per second, a VALU roofline from the algorithmic
+  FLOP count of the kernel source, and the numpy reference path (oracle in
+  the reference's literal arithmetic: einsum policy + legged_np step) timed
+  on a bounded sample of steps at the same N;
+* `cartpole_fused_k32`: the K = 32 fused CartPole step, in-kernel and array actions;
+* `es_config2`: CartPole and Acrobot fused ES rollouts, P = 4,096, H = 32, horizon 500;
+* `aba_euler`: the K-link pendulum, semi-implicit Euler dt 0.01, N = 65,536,
+  K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B).
+
+Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--sweep] [--skip-cpu] [--only cartpole|legged]
 """
 
 import argparse
@@ -41,7 +54,9 @@ for p in (str(ROOT), str(ROOT / "metal-rl-envs_amd")):
 
 METRIC = "env-steps/s at N=2^18 (CartPole, legged-4c ES rollout); % HBM/VALU roofline"
 HBM_PEAK_GBS = 8000.0
-CARTPOLE_BYTES = 41  # 16 B state in + 4 B action + 16 B state out + 4 B reward + 1 B done
+FP32_PEAK_TFLOPS = 157.3           # MI355X FP32 vector, packed (published)
+FP32_UNPACKED_TFLOPS = 78.6        # one FMA per lane per cycle
+CARTPOLE_BYTES = 41
 
 
 def log(msg):
@@ -57,11 +72,19 @@ def parse_args():
     p.add_argument("--repeats", type=int, default=3)
     p.add_argument("--fused-k", type=int, default=32)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--legged-cpu-seconds", type=float, default=12.0)
     p.add_argument("--skip-cpu", action="store_true")
-    p.add_argument("--sweep", action="store_true", help="also run the N = 2^0..2^24 sweep (to stderr and --sweep-out)")
+    p.add_argument("--only", choices=["cartpole", "legged"], default=None)
+    p.add_argument("--legged-n", type=int, default=262144)
+    p.add_argument("--legged-horizon", type=int, default=1000)
+    p.add_argument("--sweep", action="store_true", help="also run the CartPole N = 2^0..2^24 sweep")
     p.add_argument("--sweep-out", default=None)
     return p.parse_args()
 
+
+# ---------------------------------------------------------------------------
+# CartPole step
+# ---------------------------------------------------------------------------
 
 class CartPoleRun:
     """Preallocated buffers and raw C-ABI launches for the CartPole step benchmark."""
@@ -99,20 +122,8 @@ class CartPoleRun:
         if rc != 0:
             raise RuntimeError(f"hipenvs_cartpole_step_k failed: {rc}")
 
-    def capture(self, body):
-        """A HIP graph of the launches `body(stream)` enqueues."""
-        torch = self.torch
-        g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(device=self.dev)
-        side.wait_stream(torch.cuda.current_stream(self.dev))
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(g, stream=side):
-                body(self.lib.stream_of(self.dev))
-        torch.cuda.synchronize()
-        return g
-
     def graph_single(self):
-        return self.capture(lambda s: [self.launch_step(t, s) for t in range(self.steps)])
+        return capture_graph(self.dev, lambda s: [self.launch_step(t, s) for t in range(self.steps)])
 
     def graph_fused(self, k, array_actions):
         def body(s):
@@ -121,37 +132,91 @@ class CartPoleRun:
                 kk = min(k, self.steps - t)
                 self.launch_fused(t, kk, s, array_actions)
                 t += kk
-        return self.capture(body)
+        return capture_graph(self.dev, body)
 
-    def time_graph(self, g, repeats):
-        """Median wall seconds of a replay, and the HIP-event time of the same replays."""
-        torch = self.torch
-        g.replay()
+
+def capture_graph(dev, body):
+    """A HIP graph of the launches `body(stream)` enqueues on a side stream."""
+    import torch
+
+    from hipenvs import _lib
+
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            body(_lib.stream_of(dev))
+    torch.cuda.synchronize()
+    return g
+
+
+def time_replay(g, repeats):
+    """(median wall s, median HIP-event s) of graph replays; events on the replay's stream."""
+    import torch
+
+    g.replay()
+    torch.cuda.synchronize()
+    walls, events = [], []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        walls, events = [], []
-        for _ in range(repeats):
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            start.record()
-            g.replay()
-            end.record()
-            torch.cuda.synchronize()
-            walls.append(time.perf_counter() - t0)
-            events.append(start.elapsed_time(end) / 1e3)
-        return statistics.median(walls), statistics.median(events)
+        t0 = time.perf_counter()
+        start.record()
+        g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        events.append(start.elapsed_time(end) / 1e3)
+    return statistics.median(walls), statistics.median(events)
+
+
+def bench_cartpole(args, dev):
+    import torch
+
+    from hipenvs import _lib
+
+    n, steps, warmup = args.n, args.steps, args.warmup
+    run = CartPoleRun(n, steps, dev)
+    stream = _lib.stream_of(dev)
+    for t in range(warmup):
+        run.launch_step(t % steps, stream)
+    torch.cuda.synchronize()
+    g = run.graph_single()
+    wall, ev = time_replay(g, args.repeats)
+    value = n * steps / wall
+    launch = ev / steps
+    achieved = CARTPOLE_BYTES * n / launch / 1e9
+    log(f"cartpole_step N={n}: {value:,.0f} env-steps/s; {launch * 1e6:.3f} us per launch -> {achieved:.1f} GB/s")
+    gk = run.graph_fused(args.fused_k, False)
+    wk, evk = time_replay(gk, args.repeats)
+    gka = run.graph_fused(args.fused_k, True)
+    wka, evka = time_replay(gka, args.repeats)
+    k = args.fused_k
+    launches = -(-steps // k)
+    fused = {
+        "k": k,
+        "inkernel_actions_env_steps_per_s": n * steps / wk,
+        "array_actions_env_steps_per_s": n * steps / wka,
+        "inkernel_us_per_launch": evk / launches * 1e6,
+        "array_us_per_launch": evka / launches * 1e6,
+        "array_actions_algorithmic_gbs": (32 / k + 9) * n * steps / evka / 1e9,
+        "inkernel_actions_algorithmic_gbs": (32 / k + 5) * n * steps / evk / 1e9,
+    }
+    log(f"cartpole fused K={k}: in-kernel actions {fused['inkernel_actions_env_steps_per_s']:,.0f}, "
+        f"array actions {fused['array_actions_env_steps_per_s']:,.0f} env-steps/s")
+    del g, gk, gka, run
+    return value, wall, launch, achieved, fused
 
 
 def cpu_baseline_cartpole(n, seconds):
     """numpy CartPole step (reference algorithm, np.sin/np.cos) on one process; env-steps/s."""
-    import numpy as np
-
     from oracle import cartpole as oc
     from oracle import rng
 
     state = oc.reset(n, seed=0)
     actions = [rng.action_bits(t, n) for t in range(1, 9)]
-    for t in range(2):  # warm-up
+    for t in range(2):
         state, _, _ = oc.step(state, actions[t], seed=t + 1, trig="numpy")
     steps, t0 = 0, time.perf_counter()
     while True:
@@ -163,92 +228,304 @@ def cpu_baseline_cartpole(n, seconds):
     return n * steps / el, steps
 
 
-def sweep(dev, steps, k, out_path):
+def sweep(dev, steps0, k, out_path):
     rows = []
     for e in list(range(0, 21)) + [22, 24]:
         n = 1 << e
-        steps = steps if n <= (1 << 20) else 128  # keep the (steps, N) action and reward buffers a few GB
+        steps = steps0 if n <= (1 << 20) else 128  # keep the (steps, N) buffers a few GB
         run = CartPoleRun(n, steps, dev)
-        g1 = run.graph_single()
-        w1, ev1 = run.time_graph(g1, 3)
-        gk = run.graph_fused(k, False)
-        wk, _ = run.time_graph(gk, 3)
-        gka = run.graph_fused(k, True)
-        wka, _ = run.time_graph(gka, 3)
+        w1, ev1 = time_replay(run.graph_single(), 3)
+        wk, _ = time_replay(run.graph_fused(k, False), 3)
+        wka, _ = time_replay(run.graph_fused(k, True), 3)
         launch = ev1 / steps
-        row = dict(n=n, single=n * steps / w1, fused_inkernel=n * steps / wk, fused_array=n * steps / wka,
+        row = dict(n=n, steps=steps, single=n * steps / w1, fused_inkernel=n * steps / wk, fused_array=n * steps / wka,
                    launch_us=launch * 1e6, single_gbs=CARTPOLE_BYTES * n / launch / 1e9)
         rows.append(row)
         log(f"N=2^{e:<2d} single {row['single']:>16,.0f}  fused(in-kernel) {row['fused_inkernel']:>16,.0f}  "
             f"fused(array) {row['fused_array']:>16,.0f} env-steps/s  launch {row['launch_us']:7.2f} us "
             f"{row['single_gbs']:8.1f} GB/s")
-        del run, g1, gk, gka
+        del run
     if out_path:
         Path(out_path).write_text(json.dumps(rows, indent=1))
     return rows
 
 
+# ---------------------------------------------------------------------------
+# Legged ES rollout
+# ---------------------------------------------------------------------------
+
+def legged_flops_per_step(c, sweeps, hidden):
+    """Algorithmic FP32 operations per env-step of the fused legged rollout, counted from the
+    kernel source (add, sub, mul, div, sqrt = 1 each; no FMA; comparisons, selects and sign
+    flips not counted; sin/cos/tanh counted separately). N = 3 + C generalised coordinates.
+    Per substep: feet 10C, foot sums 9(C-1)+3, mass matrix 3C+4, forces 5C+11, Cholesky
+    N(N+1)(2N+1)/6, (1+2C) solves of 2N^2, free velocity 2N, Delassus 16C^2 + 8C, per sweep
+    and contact 25 (exact contact) + 6(C-1) + 2(C-2) + 2 (coupling sums), update 4CN + 2N.
+    Per step: 4 substeps + policy 2*OBS*H + 2*H*OUT + 3 for the reward bookkeeping."""
+    n = 3 + c
+    coupling = (6 * (c - 1) + 2 * max(c - 2, 0) + 2) if c > 1 else 0
+    sub = (10 * c + 9 * (c - 1) + 3 + 3 * c + 4 + 5 * c + 11 + n * (n + 1) * (2 * n + 1) // 6
+           + (1 + 2 * c) * 2 * n * n + 2 * n + 16 * c * c + 8 * c + sweeps * c * (25 + coupling) + 4 * c * n + 2 * n)
+    obs, out = 5 + 2 * c, 3 * c
+    policy = 2 * obs * hidden + 2 * hidden * out
+    return 4 * sub + policy + 3
+
+
+def legged_population(dev, p, c, hidden, sigma=0.03, seed=0):
+    """(P, D) rows: theta0 + sigma * [half; -half] around theta0 = 0.1 N(0, 1)."""
+    import torch
+
+    from hipenvs import legged_rollout
+
+    d = legged_rollout.n_params(hidden, c)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    theta0 = torch.randn(d, generator=g, device=dev) * 0.1
+    half = torch.randn((p // 2, d), generator=g, device=dev)
+    return theta0[None, :] + sigma * torch.cat([half, -half], dim=0)
+
+
+def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats):
+    """(median wall s, median HIP-event s, steps taken, mean fitness) of full rollouts."""
+    import torch
+
+    from hipenvs import legged_rollout
+
+    cols = schedule in ("columns", "chunked")
+    small = theta[:, :64].contiguous() if cols else theta[:64].contiguous()
+    kw = {"theta_cols": small} if schedule == "chunked" else {}
+    legged_rollout.rollout(state[:, :64].contiguous(), None if kw else small, hidden, 4, c, iters=sweeps,
+                           schedule=schedule, **kw)
+    torch.cuda.synchronize()
+    walls, evs, taken, fit = [], [], None, None
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        kw = {"theta_cols": theta} if schedule == "chunked" else {}
+        fit, steps = legged_rollout.rollout(state, None if kw else theta, hidden, horizon, c, iters=sweeps,
+                                            schedule=schedule, **kw)
+        end.record()
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        evs.append(start.elapsed_time(end) / 1e3)
+        taken = float(steps.double().sum().item())
+    return statistics.median(walls), statistics.median(evs), taken, float(fit.mean().item())
+
+
+def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
+    from hipenvs import legged, legged_rollout
+
+    c, hidden, p, horizon = 4, 64, args.legged_n, args.legged_horizon
+    theta = legged_population(dev, p, c, hidden)
+    theta_cols = theta.T.contiguous()
+    state = legged.Legged(c).reset(p, seed=0, device=dev)
+    d = legged_rollout.n_params(hidden, c)
+    out = {"n_envs": p, "c": c, "hidden": hidden, "horizon": horizon, "sigma": 0.03, "alive_bonus": 1.0,
+           "schedule": f"chunked ({legged_rollout.CHUNK_STEPS} steps), columns layout", "by_sweeps": {}}
+    for s in sweeps_list:
+        wall, ev, taken, fit_mean = time_rollout(state, theta_cols, hidden, horizon, c, s, "chunked", args.repeats)
+        flops = legged_flops_per_step(c, s, hidden)
+        achieved_tf = taken * flops / ev / 1e12
+        rec = {
+            "env_steps_per_s": taken / wall,
+            "steps_taken": taken,
+            "mean_episode": taken / p,
+            "wall_s": wall,
+            "kernel_event_s": ev,
+            "flops_per_env_step": flops,
+            "roofline": {"bound": "valu", "achieved": achieved_tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": achieved_tf / FP32_PEAK_TFLOPS,
+                         "frac_of_unpacked_peak": achieved_tf / FP32_UNPACKED_TFLOPS, "traffic": None},
+            "weight_bytes_per_env_step": 4 * d,
+            "weight_stream_gbs": taken * 4 * d / ev / 1e9,
+            "fitness_mean": fit_mean,
+        }
+        out["by_sweeps"][str(s)] = rec
+        log(f"legged4 ES rollout N={p} H={hidden} S={s} (chunked): {rec['env_steps_per_s']:,.0f} env-steps/s "
+            f"(mean episode {taken / p:.1f} steps, {ev * 1e3:.1f} ms), {achieved_tf:.2f} TFLOP/s algorithmic, "
+            f"weights read at {rec['weight_stream_gbs']:.0f} GB/s")
+    wall, ev, taken, _ = time_rollout(state, theta, hidden, horizon, c, 8, "rows", 1)
+    out["static_rows_s8_env_steps_per_s"] = taken / wall
+    del theta
+    wall, ev, taken, _ = time_rollout(state, theta_cols, hidden, horizon, c, 8, "columns", 1)
+    out["static_columns_s8_env_steps_per_s"] = taken / wall
+    log(f"legged4 one member per lane, S=8: rows {out['static_rows_s8_env_steps_per_s']:,.0f}, "
+        f"columns {out['static_columns_s8_env_steps_per_s']:,.0f} env-steps/s")
+    del theta_cols
+    return out
+
+
+def cpu_baseline_legged(n, seconds, c=4, hidden=64, sweeps=8):
+    """The reference's numpy ES path at N members: einsum policy (es.py:167-171), per-leg
+    argmax (es.py:86-93), legged_np step in its literal arithmetic; steps per second."""
+    import numpy as np
+
+    from oracle import es as oes
+    from oracle import legged as olg
+
+    body = olg.Legged(c, sweeps, mode="reference")
+    state = body.reset(n, seed=0)
+    r = np.random.default_rng(0)
+    d = oes.n_params(hidden, 5 + 2 * c, 3 * c)
+    theta0 = (r.standard_normal(d, dtype=np.float32) * np.float32(0.1))
+    half = r.standard_normal((n // 2, d), dtype=np.float32)
+    theta = theta0[None, :] + np.float32(0.03) * np.concatenate([half, -half])
+    del half
+    w1, b1, w2, b2 = oes.unflatten(theta, hidden, 5 + 2 * c, 3 * c)
+
+    def one(t, state):
+        obs = state[1:].T
+        h = np.tanh(np.einsum("pi,pih->ph", obs, w1) + b1)
+        logits = np.einsum("ph,pho->po", h, w2) + b2
+        return body.step(state, oes.legged_action(logits, c), seed=t)[0]
+
+    state = one(1, state)  # warm-up
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        state = one(steps + 2, state)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return n * steps / el, steps
+
+
+# ---------------------------------------------------------------------------
+# ES config 2 and ABA config 3
+# ---------------------------------------------------------------------------
+
+def bench_es_config2(dev, repeats):
+    import torch
+
+    from hipenvs import acrobot, acrobot_rollout, cartpole, cartpole_rollout
+
+    out = {}
+    for name, env, mod, d_of in (("cartpole", cartpole, cartpole_rollout, lambda h: 7 * h + 2),
+                                 ("acrobot", acrobot, acrobot_rollout, lambda h: 10 * h + 3)):
+        p, hidden, horizon = 4096, 32, 500
+        g = torch.Generator(device=dev).manual_seed(0)
+        theta0 = torch.randn(d_of(hidden), generator=g, device=dev) * 0.1
+        half = torch.randn((p // 2, d_of(hidden)), generator=g, device=dev)
+        theta = theta0[None, :] + 0.1 * torch.cat([half, -half])
+        state = env.reset(p, seed=0, device=dev)
+        mod.rollout_steps(state, theta, hidden, horizon)
+        walls, survived = [], None
+        for _ in range(repeats):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            survived = mod.rollout_steps(state, theta, hidden, horizon)
+            torch.cuda.synchronize()
+            walls.append(time.perf_counter() - t0)
+        wall = statistics.median(walls)
+        taken = float(torch.clamp(survived + 1, max=horizon).sum().item())
+        out[name] = {"P": p, "hidden": hidden, "horizon": horizon, "rollout_s": wall,
+                     "steps_taken_per_s": taken / wall, "p_x_horizon_per_s": p * horizon / wall,
+                     "mean_steps_survived": float(survived.mean().item())}
+        log(f"ES {name} P={p} H={hidden}: {taken / wall:,.0f} steps-taken/s, {p * horizon / wall:,.0f} PxH/s "
+            f"({wall * 1e3:.2f} ms per rollout)")
+    return out
+
+
+def bench_aba(dev, steps=1000, n=65536, ks=(4, 16, 64)):
+    import torch
+
+    from hipenvs import _lib, pendulum_aba
+
+    out = {}
+    for k in ks:
+        p = pendulum_aba.Pendulum(k)
+        bufs = [p.reset(n, seed=0, device=dev, zero_velocity=True), torch.empty((2 * k, n), device=dev)]
+        reward = torch.empty(n, device=dev)
+        done = torch.empty(n, dtype=torch.bool, device=dev)
+        fn = _lib.lib().hipenvs_pendulum_aba_step_euler
+        P = _lib.ptr
+
+        def body(s):
+            for t in range(steps):
+                rc = fn(k, P(bufs[t % 2]), P(None), t + 1, P(bufs[(t + 1) % 2]), P(reward), P(done), n, s)
+                if rc != 0:
+                    raise RuntimeError(f"aba step failed: {rc}")
+
+        g = capture_graph(dev, body)
+        wall, ev = time_replay(g, 3)
+        launch = ev / steps
+        bytes_step = 16 * k + 9
+        achieved = bytes_step * n / launch / 1e9
+        out[str(k)] = {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
+                       "bytes_per_env_step": bytes_step,
+                       "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                    "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
+        log(f"ABA Euler K={k} N={n}: {n * steps / wall:,.0f} env-steps/s, {launch * 1e6:.2f} us per launch, "
+            f"{achieved:.0f} GB/s algorithmic")
+        del g, bufs
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the hot path has no "
-              f"cross-GPU work; see the sharding note in the design document)", file=sys.stderr)
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the hot path has no "
+              f"cross-GPU work (every environment and member is independent)", file=sys.stderr)
         sys.exit(2)
     import torch
 
     from hipenvs import _lib
 
     dev = torch.device("cuda", 0)
-    n, steps, warmup = args.n, args.steps, args.warmup
-    log(f"hipenvs: {_lib.version()} on {torch.cuda.get_device_name(dev)}; N={n} steps={steps} warmup={warmup}")
-
-    run_t = CartPoleRun(n, steps, dev)
-    stream = _lib.stream_of(dev)
-    for t in range(warmup):  # untimed eager steps: module load, clocks, caches
-        run_t.launch_step(t % steps, stream)
-    torch.cuda.synchronize()
-    g = run_t.graph_single()
-    wall, ev = run_t.time_graph(g, args.repeats)
-    value = n * steps / wall
-    log(f"single-step kernel, graph replay: {value:,.0f} env-steps/s ({wall * 1e3:.3f} ms for {steps} steps)")
-    launch = ev / steps  # average launch duration: HIP events around the timed replay, on its stream
-    achieved = CARTPOLE_BYTES * n / launch / 1e9
-    log(f"cartpole_step: {launch * 1e6:.3f} us per launch (HIP events over the timed region) "
-        f"-> {achieved:.1f} GB/s algorithmic")
-    gk = run_t.graph_fused(args.fused_k, False)
-    wk, _ = run_t.time_graph(gk, args.repeats)
-    gka = run_t.graph_fused(args.fused_k, True)
-    wka, _ = run_t.time_graph(gka, args.repeats)
-    log(f"fused K={args.fused_k}: in-kernel actions {n * steps / wk:,.0f}, array actions {n * steps / wka:,.0f} env-steps/s")
-
-    extra = {
-        "single_step_timed_region_event_s": ev,
-        "cartpole_step_us_per_launch": launch * 1e6,
-        f"fused_k{args.fused_k}_inkernel_actions_env_steps_per_s": n * steps / wk,
-        f"fused_k{args.fused_k}_array_actions_env_steps_per_s": n * steps / wka,
-        f"fused_k{args.fused_k}_array_actions_algorithmic_gbs": (32 / args.fused_k + 9) * n * steps / wka / 1e9,
-    }
-    if args.sweep:
-        extra["sweep"] = sweep(dev, steps, args.fused_k, args.sweep_out)
+    log(f"hipenvs: {_lib.version()} on {torch.cuda.get_device_name(dev)}; host os.cpu_count()={os.cpu_count()}")
+    extra = {}
+    value = wall = launch = achieved = None
+    if args.only in (None, "cartpole"):
+        value, wall, launch, achieved, fused = bench_cartpole(args, dev)
+        extra["cartpole_fused_k32"] = fused
+        extra["cartpole_step_us_per_launch"] = launch * 1e6
+        if args.sweep:
+            extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out)
+    if args.only in (None, "legged"):
+        legged = bench_legged(args, dev)
+        if not args.skip_cpu:
+            rate, csteps = cpu_baseline_legged(args.legged_n, args.legged_cpu_seconds)
+            legged["cpu_baseline"] = {
+                "value": rate, "unit": "env-steps/s", "cores": 1, "kind": "port",
+                "sample": f"numpy ES step (einsum policy + legged step in the reference's literal arithmetic), "
+                          f"N={args.legged_n}, C=4, H=64, S=8, {csteps} timed steps after 1 warm-up"}
+            legged["speedup_vs_cpu_s8"] = legged["by_sweeps"]["8"]["env_steps_per_s"] / rate
+            log(f"legged numpy baseline: {rate:,.0f} env-steps/s -> GPU/CPU {legged['speedup_vs_cpu_s8']:,.0f}x")
+        extra["legged4_es_rollout"] = legged
+    if args.only is None:
+        extra["es_config2"] = bench_es_config2(dev, args.repeats)
+        extra["aba_euler"] = bench_aba(dev)
 
     cpu = None
-    if not args.skip_cpu:
-        rate, csteps = cpu_baseline_cartpole(n, args.cpu_seconds)
+    if not args.skip_cpu and args.only in (None, "cartpole"):
+        rate, csteps = cpu_baseline_cartpole(args.n, args.cpu_seconds)
         cpu = {"value": rate, "unit": "env-steps/s", "cores": 1, "kind": "port",
-               "sample": f"numpy CartPole step (reference op order, np.sin/np.cos), N={n}, {csteps} steps, "
+               "sample": f"numpy CartPole step (reference op order, np.sin/np.cos), N={args.n}, {csteps} steps, "
                          f"single process on a host with os.cpu_count()={os.cpu_count()}"}
-        log(f"cpu baseline: {rate:,.0f} env-steps/s over {csteps} steps")
+        log(f"cartpole numpy baseline: {rate:,.0f} env-steps/s over {csteps} steps")
 
+    if value is None:  # --only legged: the legged rollout is the line
+        rec = extra["legged4_es_rollout"]["by_sweeps"]["8"]
+        value, wall = rec["env_steps_per_s"], rec["wall_s"]
+        roofline = rec["roofline"]
+        cpu = extra["legged4_es_rollout"].get("cpu_baseline")
+        config = {"workload": f"legged4 ES rollout, N={args.legged_n}, H=64, S=8, horizon {args.legged_horizon}",
+                  "n_envs": args.legged_n}
+        ms = wall * 1e3
+        steps = args.legged_horizon
+    else:
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBS, "traffic": None}
+        config = {"workload": f"cartpole_step, N={args.n}, {args.steps} steps, one launch per step (HIP graph replay)",
+                  "n_envs": args.n, "parallelism": "single GPU, one thread per 4 envs"}
+        ms = wall * 1e3 / args.steps
+        steps = args.steps
     line = {
-        "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
-        "ms_per_step": wall * 1e3 / steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp32", "data": "synthetic (counter-RNG states and Bernoulli(0.5) actions)",
-        "config": {"workload": f"cartpole_step, N={n}, {steps} steps, one launch per step (HIP graph replay)",
-                   "n_envs": n, "parallelism": "single GPU, one thread per 4 envs"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
-        "cpu_baseline": cpu,
-        "extra": extra,
+        "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic (counter-RNG states and actions, seeded Gaussian ES populations)",
+        "config": config, "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(line), flush=True)
 

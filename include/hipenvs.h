@@ -188,6 +188,25 @@ int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iters, int32_t 
                               float fall_penalty, float height_gate, double assist, float* fitness, float* steps,
                               hipenvs_stream_t stream);
 
+/* Bytes of device workspace hipenvs_legged_es_rollout_chunked needs for p
+ * members: two packed member sets (state, weights, accumulators, ids) and two
+ * counters; -1 for an unsupported c or hidden. */
+int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t hidden, int64_t p);
+
+/* The same rollout, scheduled in chunks of `chunk_steps` steps: after each
+ * chunk the surviving members (state, accumulators and weights) are packed
+ * into a dense column buffer in `workspace`, so later chunks run full waves
+ * despite heavy-tailed episode lengths; the counts stay on the device and the
+ * whole rollout is enqueued without a host round trip. theta_cols is (D, p)
+ * columns; p < 2^31; workspace_bytes >= hipenvs_legged_es_rollout_workspace_bytes.
+ * Results identical to hipenvs_legged_es_rollout. Calls that share a workspace
+ * must not overlap. */
+int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
+                                      const float* state, const float* theta_cols, int64_t p, int32_t horizon,
+                                      float alive_bonus, float fall_penalty, float height_gate, double assist,
+                                      float* fitness, float* steps, void* workspace, int64_t workspace_bytes,
+                                      hipenvs_stream_t stream);
+
 /* ---- Diagnostics (no reference counterpart) ---------------------------- */
 
 /* Elementwise deterministic sin, cos, tanh of x (n) as the kernels compute them;

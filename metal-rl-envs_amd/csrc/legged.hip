@@ -222,6 +222,45 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
   return (q[1] < FALL_HEIGHT) || (fabsf(q[2]) > FALL_ANGLE);
 }
 
+// The member's (5+2C)-HID-3C tanh policy and per-leg torques (legged_rollout_metal.py:217-236).
+// Weight d of the member is w[d * stride]. Every accumulator sums in the reference
+// kernel's order (hidden unit j: bias, then the observations in order; head o:
+// bias, then the hidden units in order). POLICY_UNROLL hidden units per loop
+// iteration bounds how many of the member's weight loads are in flight at once.
+#ifndef POLICY_UNROLL
+#define POLICY_UNROLL 2
+#endif
+template <int C, int HID>
+__device__ __forceinline__ void policy_torques(const float* __restrict__ w, int64_t stride, const float (&q)[3 + C],
+                                               const float (&v)[3 + C], float (&tq)[C]) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int B1 = OBS * HID, W2 = B1 + HID, B2 = W2 + HID * OUT;
+  float obs[OBS];
+#pragma unroll
+  for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
+#pragma unroll
+  for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
+  float logit[OUT];
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) logit[o] = w[(B2 + o) * stride];
+#pragma unroll POLICY_UNROLL
+  for (int j = 0; j < HID; ++j) {
+    float s = w[(B1 + j) * stride];
+#pragma unroll
+    for (int k = 0; k < OBS; ++k) s = s + obs[k] * w[(k * HID + j) * stride];
+    const float hj = det_tanh(s);
+#pragma unroll
+    for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w[(W2 + j * OUT + o) * stride];
+  }
+#pragma unroll
+  for (int leg = 0; leg < C; ++leg) {
+    float torque = -1.0f, best = logit[3 * leg];
+    if (logit[3 * leg + 1] > best) { torque = 0.0f; best = logit[3 * leg + 1]; }
+    if (logit[3 * leg + 2] > best) { torque = 1.0f; }
+    tq[leg] = torque * TORQUE;
+  }
+}
+
 template <int C>
 __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ state,
                                                       const int32_t* __restrict__ action, uint32_t seed,
@@ -292,30 +331,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
   }
   float total = 0.0f, taken = 0.0f;
   for (int32_t t = 0; t < horizon; ++t) {
-    float obs[OBS];
-#pragma unroll
-    for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
-#pragma unroll
-    for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
-    float logit[OUT];
-#pragma unroll
-    for (int o = 0; o < OUT; ++o) logit[o] = w[(B2 + o) * stride];
-#pragma unroll 2
-    for (int j = 0; j < HID; ++j) {
-      float s = w[(B1 + j) * stride];
-#pragma unroll
-      for (int k = 0; k < OBS; ++k) s = s + obs[k] * w[(k * HID + j) * stride];
-      const float hj = det_tanh(s);
-#pragma unroll
-      for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w[(W2 + j * OUT + o) * stride];
-    }
-#pragma unroll
-    for (int leg = 0; leg < C; ++leg) {
-      float torque = -1.0f, best = logit[3 * leg];
-      if (logit[3 * leg + 1] > best) { torque = 0.0f; best = logit[3 * leg + 1]; }
-      if (logit[3 * leg + 2] > best) { torque = 1.0f; }
-      tq[leg] = torque * TORQUE;
-    }
+    policy_torques<C, HID>(w, stride, q, v, tq);
 #pragma unroll 1
     for (int s = 0; s < SUBSTEPS; ++s) substep<C>(q, v, tq, iters, assist, assist_damping);
     if (fallen<C>(q)) {
@@ -328,6 +344,179 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
   }
   fitness[e] = total;
   steps_out[e] = taken;
+}
+
+// Compacting schedule for the fused rollout. Episode lengths are heavy-tailed
+// (at the ES benchmark's shape the mean is ~43 steps while a few members last
+// the whole horizon), and a one-member-per-lane launch keeps each wave busy
+// until its longest member ends. Here the rollout runs in chunks of
+// `chunk_steps` steps. Each chunk reads a packed set of members in the column
+// layout (D, cap), so a wave's loads of one weight stay 256 contiguous bytes.
+// The survivors of a chunk are appended to the other packed buffer, with their
+// state, accumulators and weights, at slots taken from a wave-aggregated atomic
+// counter. The first chunk reads the caller's state and columns directly.
+// Counts stay on the device: later chunks run a grid-stride loop over whatever
+// count the previous chunk left, so the whole rollout is enqueued without a
+// host round trip. Every loop is bounded (a member runs at most `horizon`
+// steps, a chunk at most `chunk_steps`), and each member's arithmetic is the
+// same as in the one-member-per-lane kernel, whatever slot it lands in.
+struct Packed {
+  float* state;      // (2N, cap): q then v
+  float* theta;      // (D, cap)
+  float* acc;        // (2, cap): total, taken
+  int32_t* meta;     // (2, cap): member id, steps done
+  uint32_t* count;
+};
+
+template <int C, int HID, bool kFirst>
+__global__ __launch_bounds__(64) void rollout_chunk_kernel(const float* __restrict__ state0,
+                                                           const float* __restrict__ theta0, int64_t p,
+                                                           Packed src, Packed dst, int64_t cap,
+                                                           int32_t chunk_steps, int32_t horizon, int iters,
+                                                           float alive_bonus, float fall, float gate, float assist,
+                                                           float assist_damping, float* __restrict__ fitness,
+                                                           float* __restrict__ steps_out) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  constexpr int B1 = OBS * HID, W2 = B1 + HID, B2 = W2 + HID * OUT;
+  const unsigned lane = threadIdx.x;
+  const int64_t count = kFirst ? p : (int64_t)*src.count;
+  const int64_t src_stride = kFirst ? p : cap;
+  const float* sstate = kFirst ? state0 : src.state;
+  const float* stheta = kFirst ? theta0 : src.theta;
+  for (int64_t base = (int64_t)blockIdx.x * 64; base < count; base += (int64_t)gridDim.x * 64) {
+    const int64_t i = base + lane;
+    bool live = i < count;
+    float q[N], v[N], tq[C];
+    float total = 0.0f, taken = 0.0f;
+    int32_t id = 0, t = 0;
+    if (live) {
+#pragma unroll
+      for (int r = 0; r < N; ++r) {
+        q[r] = sstate[r * src_stride + i];
+        v[r] = sstate[(N + r) * src_stride + i];
+      }
+      if (kFirst) {
+        id = (int32_t)i;
+      } else {
+        total = src.acc[i];
+        taken = src.acc[cap + i];
+        id = src.meta[i];
+        t = src.meta[cap + i];
+      }
+    }
+    const float* w = stheta + i;
+    for (int32_t k = 0; k < chunk_steps; ++k) {
+      if (!__any(live)) break;
+      if (!live) continue;
+      policy_torques<C, HID>(w, src_stride, q, v, tq);
+#pragma unroll 1
+      for (int sub = 0; sub < SUBSTEPS; ++sub) substep<C>(q, v, tq, iters, assist, assist_damping);
+      ++t;
+      bool finished;
+      if (fallen<C>(q)) {
+        taken += 1.0f;
+        total = total - fall;
+        finished = true;
+      } else {
+        total = total + (((q[1] >= gate) ? v[0] : 0.0f) + alive_bonus);
+        taken += 1.0f;
+        finished = t >= horizon;
+      }
+      if (finished) {
+        fitness[id] = total;
+        steps_out[id] = taken;
+        live = false;
+      }
+    }
+    // append the survivors to the destination set
+    const unsigned long long m = __ballot(live);
+    if (m) {
+      const int leader = __ffsll((long long)m) - 1;
+      unsigned int slot0 = 0;
+      if ((int)lane == leader) slot0 = atomicAdd(dst.count, (unsigned int)__popcll(m));
+      slot0 = __shfl(slot0, leader);
+      if (live) {
+        const int64_t slot = (int64_t)slot0 + __popcll(m & ((1ull << lane) - 1ull));
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+          dst.state[r * cap + slot] = q[r];
+          dst.state[(N + r) * cap + slot] = v[r];
+        }
+        dst.acc[slot] = total;
+        dst.acc[cap + slot] = taken;
+        dst.meta[slot] = id;
+        dst.meta[cap + slot] = t;
+        for (int d = 0; d < D; ++d) dst.theta[d * cap + slot] = w[d * src_stride];
+      }
+    }
+  }
+}
+
+__global__ void set_count_kernel(uint32_t* count, uint32_t value) { *count = value; }
+
+template <int C, int HID>
+int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32_t horizon, int iters,
+                   int32_t chunk_steps, float alive, float fall, float gate, double assist, float* fitness,
+                   float* steps, void* workspace, hipStream_t s) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  const int64_t cap = p;
+  // carve the workspace: two packed sets, then two counters
+  char* ws = static_cast<char*>(workspace);
+  Packed set[2];
+  for (int b = 0; b < 2; ++b) {
+    set[b].state = reinterpret_cast<float*>(ws);
+    ws += sizeof(float) * 2 * N * cap;
+    set[b].theta = reinterpret_cast<float*>(ws);
+    ws += sizeof(float) * (int64_t)D * cap;
+    set[b].acc = reinterpret_cast<float*>(ws);
+    ws += sizeof(float) * 2 * cap;
+    set[b].meta = reinterpret_cast<int32_t*>(ws);
+    ws += sizeof(int32_t) * 2 * cap;
+  }
+  set[0].count = reinterpret_cast<uint32_t*>(ws);
+  set[1].count = set[0].count + 1;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rollout_chunk_kernel<C, HID, false>, 64, 0) !=
+          hipSuccess)
+    return launch_status();
+  const int64_t needed = (p + 63) / 64;
+  int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
+  const float af = (float)assist, ad = (float)(0.1 * assist);
+  // first chunk: the caller's arrays -> set 0
+  hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
+  hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true>), dim3((unsigned)needed), dim3(64), 0, s, state, theta_cols,
+                     p, set[1], set[0], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps);
+  int status = launch_status();
+  int cur = 0;
+  const int64_t grid = resident < needed ? resident : needed;
+  for (int64_t done = chunk_steps; status == HIPENVS_OK && done < horizon; done += chunk_steps) {
+    const int nxt = 1 - cur;
+    hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[nxt].count, 0u);
+    hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state, theta_cols,
+                       p, set[cur], set[nxt], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness,
+                       steps);
+    status = launch_status();
+    cur = nxt;
+  }
+  return status;
+}
+
+template <int C>
+int dispatch_chunked(int32_t hidden, const float* state, const float* theta_cols, int64_t p, int32_t horizon,
+                     int iters, int32_t chunk_steps, float alive, float fall, float gate, double assist,
+                     float* fitness, float* steps, void* workspace, hipStream_t s) {
+  switch (hidden) {
+    case 4: return launch_chunked<C, 4>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 8: return launch_chunked<C, 8>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 16: return launch_chunked<C, 16>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 32: return launch_chunked<C, 32>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 64: return launch_chunked<C, 64>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
 }
 
 template <int C>
@@ -419,6 +608,39 @@ extern "C" int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iter
     case 1: return lg::dispatch_hidden<1>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
     case 2: return lg::dispatch_hidden<2>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
     case 4: return lg::dispatch_hidden<4>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+
+extern "C" int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t hidden, int64_t p) {
+  if (p < 0 || (c != 1 && c != 2 && c != 4) || (hidden != 4 && hidden != 8 && hidden != 16 && hidden != 32 &&
+                                                hidden != 64))
+    return -1;
+  const int64_t n = 3 + c, obs = 5 + 2 * c, out = 3 * c;
+  const int64_t d = obs * hidden + hidden + hidden * out + out;
+  return 2 * (2 * n + d + 4) * p * 4 + 64;
+}
+
+extern "C" int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
+                                                 const float* state, const float* theta_cols, int64_t p,
+                                                 int32_t horizon, float alive_bonus, float fall_penalty,
+                                                 float height_gate, double assist, float* fitness, float* steps,
+                                                 void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream) {
+  if (p < 0 || horizon < 0 || iters < 0 || iters > kMaxIters || chunk_steps < 1 || p > 0x7fffffffLL ||
+      (p > 0 && (!state || !theta_cols || !fitness || !steps || !workspace)))
+    return HIPENVS_E_ARG;
+  if (p == 0) return HIPENVS_OK;
+  const int64_t need = hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p);
+  if (need < 0) return HIPENVS_E_UNSUPPORTED;
+  if (workspace_bytes < need) return HIPENVS_E_ARG;
+  if (horizon == 0)  // nothing to step: every member scores 0 in 0 steps
+    return hipenvs_legged_es_rollout(c, hidden, iters, 1, state, theta_cols, p, 0, alive_bonus, fall_penalty,
+                                     height_gate, assist, fitness, steps, stream);
+  hipStream_t s = as_stream(stream);
+  switch (c) {
+    case 1: return lg::dispatch_chunked<1>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 2: return lg::dispatch_chunked<2>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 4: return lg::dispatch_chunked<4>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
 }

@@ -8,8 +8,9 @@
 // bias pa = p + Ia c + U u / D folded into the parent through X^T (.) X; outward
 // accelerations with the base accelerating at -g; the running sum turns joint
 // accelerations into absolute ones. Per link the kernel keeps cos/sin of the
-// joint angle, the link velocity and U, u (9 floats); K is a template constant
-// so every per-link array is indexed statically and lives in VGPRs/AGPRs.
+// joint angle, the link velocity and U, u (9 floats); K is a template constant,
+// and for K <= 16 every per-link array is indexed statically and lives in
+// VGPRs/AGPRs.
 //
 // Algorithmic bytes per env-step: 2K floats in, 2K floats out, 4 B action or
 // torque, 4 B reward, 1 B done = 16K + 9 B.
@@ -31,6 +32,11 @@ constexpr float PI = 0x1.921fb6p+1f;          // float32(pi)
 
 __device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf((x + PI) / TWO_PI); }
 
+// Per-link loops are unrolled (U = K), so every per-link array is a set of
+// registers, except in the RK4 step past K = 16: its four chained evaluations no
+// longer fit the register file, so there the loops stay rolled (U = 1) and the
+// per-link arrays live in private (scratch) memory.
+
 // Velocity-product bias p = v x* (I v) of a unit mass at (1, 0) (pendulum_aba_np.py:46-47).
 __device__ __forceinline__ void own_bias(float w, float x, float y, float& p0, float& p1, float& p2) {
   const float f = w + y;
@@ -40,13 +46,13 @@ __device__ __forceinline__ void own_bias(float w, float x, float y, float& p0, f
 }
 
 // Absolute angular accelerations acc[K] from absolute angles th[K] and velocities om[K].
-template <int K>
+template <int K, int U = K>
 __device__ __forceinline__ void accelerations(const float* th, const float* om, float torque, float* acc) {
   float cs[K], sn[K], vw[K], vx[K], vy[K], U0[K], U1[K], U2[K], uu[K];
   // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
   {
     float w = 0.0f, x = 0.0f, y = 0.0f;
-#pragma unroll
+#pragma unroll U
     for (int i = 0; i < K; ++i) {
       const int im = i > 0 ? i - 1 : 0;
       const float q = (i == 0) ? th[0] : th[i] - th[im];
@@ -70,7 +76,7 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
     float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
     float P0, P1, P2;
     own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
-#pragma unroll
+#pragma unroll U
     for (int i = K - 1; i >= 0; --i) {
       U0[i] = A0;
       U1[i] = A1;
@@ -113,7 +119,7 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
   // outward: accelerations from a base accelerating at -g (pendulum_aba_np.py:83-99)
   {
     float aw = 0.0f, ax = -GRAVITY, ay = 0.0f, run = 0.0f;
-#pragma unroll
+#pragma unroll U
     for (int i = 0; i < K; ++i) {
       const int im = i > 0 ? i - 1 : 0;
       const float c = cs[i], s = sn[i];
@@ -134,44 +140,44 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
 }
 
 // Tip above half the chain's length: -(sum_i cos th_i) > K / 2 (pendulum_np.py:81-82).
-template <int K>
+template <int K, int U = K>
 __device__ __forceinline__ bool terminal(const float* th) {
   float s = 0.0f;
-#pragma unroll
+#pragma unroll U
   for (int i = 0; i < K; ++i) s = (i == 0) ? det_cos(th[0]) : s + det_cos(th[i]);
   return -s > (float)K * 0.5f;
 }
 
 // RK4 at dt 0.02 in place (pendulum_aba_np.py:117-123), stage sums accumulated in numpy's order.
-template <int K>
+template <int K, int U = (K <= 16 ? K : 1)>
 __device__ __forceinline__ void rk4(float* th, float* om, float torque) {
   float acc[K], t[K], o[K], sth[K], som[K];
-  accelerations<K>(th, om, torque, acc);
-#pragma unroll
+  accelerations<K, U>(th, om, torque, acc);
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     sth[p] = om[p];
     som[p] = acc[p];
     t[p] = th[p] + DT_2 * om[p];
     o[p] = om[p] + DT_2 * acc[p];
   }
-  accelerations<K>(t, o, torque, acc);
-#pragma unroll
+  accelerations<K, U>(t, o, torque, acc);
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     sth[p] = sth[p] + 2.0f * o[p];
     som[p] = som[p] + 2.0f * acc[p];
     t[p] = th[p] + DT_2 * o[p];
     o[p] = om[p] + DT_2 * acc[p];
   }
-  accelerations<K>(t, o, torque, acc);
-#pragma unroll
+  accelerations<K, U>(t, o, torque, acc);
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     sth[p] = sth[p] + 2.0f * o[p];
     som[p] = som[p] + 2.0f * acc[p];
     t[p] = th[p] + DT * o[p];
     o[p] = om[p] + DT * acc[p];
   }
-  accelerations<K>(t, o, torque, acc);
-#pragma unroll
+  accelerations<K, U>(t, o, torque, acc);
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     th[p] = wrap(th[p] + DT_6 * (sth[p] + o[p]));
     om[p] = clip(om[p] + DT_6 * (som[p] + acc[p]), -MAX_VEL, MAX_VEL);
@@ -179,11 +185,11 @@ __device__ __forceinline__ void rk4(float* th, float* om, float torque) {
 }
 
 // Semi-implicit Euler at dt 0.01 in place: omega first, then theta with the new omega.
-template <int K>
+template <int K, int U = K>
 __device__ __forceinline__ void euler(float* th, float* om, float torque) {
   float acc[K];
   accelerations<K>(th, om, torque, acc);
-#pragma unroll
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     const float om_new = om[p] + DT_EULER * acc[p];
     const float th_new = th[p] + DT_EULER * om_new;
@@ -192,9 +198,9 @@ __device__ __forceinline__ void euler(float* th, float* om, float torque) {
   }
 }
 
-template <int K>
+template <int K, int U = K>
 __device__ __forceinline__ void load(const float* __restrict__ state, int64_t n, int64_t e, float* th, float* om) {
-#pragma unroll
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     th[p] = state[p * n + e];
     om[p] = state[(K + p) * n + e];
@@ -203,16 +209,16 @@ __device__ __forceinline__ void load(const float* __restrict__ state, int64_t n,
 
 // Masked reset: all 2K rows U[+-0.1] (RK4 task) or angles U[+-0.1] and zero velocities (Euler task),
 // row p of env e hashed at (seed ^ e*golden) + p * 0x85EBCA6B (pendulum_aba_metal.py:109-113).
-template <int K, bool kZeroVelocity>
+template <int K, bool kZeroVelocity, int U = K>
 __device__ __forceinline__ void store_with_reset(float* __restrict__ next, int64_t n, int64_t e, const float* th,
                                                  const float* om, bool d, uint32_t seed) {
   const uint32_t h = env_hash(seed, (uint32_t)e);
-#pragma unroll
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     const float fresh = uniform_pm(pcg_hash(h + (uint32_t)p * kRowStride), RESET_BOUND);
     next[p * n + e] = d ? fresh : th[p];
   }
-#pragma unroll
+#pragma unroll U
   for (int p = 0; p < K; ++p) {
     const float fresh = kZeroVelocity ? 0.0f : uniform_pm(pcg_hash(h + (uint32_t)(K + p) * kRowStride), RESET_BOUND);
     next[(K + p) * n + e] = d ? fresh : om[p];
@@ -226,11 +232,12 @@ __global__ __launch_bounds__(kBlock) void step_rk4_kernel(const float* __restric
                                                           uint8_t* __restrict__ done, int64_t n) {
   const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (e >= n) return;
+  constexpr int U = K <= 16 ? K : 1;
   float th[K], om[K];
-  load<K>(state, n, e, th, om);
-  rk4<K>(th, om, (float)(action[e] - 1) * 1.0f);
-  const bool d = terminal<K>(th);
-  store_with_reset<K, false>(next, n, e, th, om, d, seed);
+  load<K, U>(state, n, e, th, om);
+  rk4<K, U>(th, om, (float)(action[e] - 1) * 1.0f);
+  const bool d = terminal<K, U>(th);
+  store_with_reset<K, false, U>(next, n, e, th, om, d, seed);
   reward[e] = d ? 0.0f : -1.0f;
   done[e] = d ? 1 : 0;
 }

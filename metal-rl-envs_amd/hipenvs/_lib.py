@@ -43,6 +43,13 @@ SIGNATURES = {
     "hipenvs_legged_step": [_I32, _I32, ctypes.c_double, _P, _P, _U32, _P, _P, _P, _P, _I64, _P],
     "hipenvs_legged_es_rollout": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32, ctypes.c_double,
                                   _P, _P, _P],
+    "hipenvs_legged_es_rollout_chunked": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32,
+                                          ctypes.c_double, _P, _P, _P, _I64, _P],
+}
+
+# entry points that return a value rather than a status
+VALUE_SIGNATURES = {
+    "hipenvs_legged_es_rollout_workspace_bytes": (ctypes.c_int64, [_I32, _I32, _I64]),
 }
 
 
@@ -67,6 +74,10 @@ def lib():
         for name, argtypes in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        for name, (restype, argtypes) in VALUE_SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
             fn.argtypes = argtypes
         _lib = handle
     return _lib

@@ -8,9 +8,20 @@ accumulating the shaped reward (forward velocity while the torso is above
 pays ``fall_penalty`` once. Returns (fitness, steps taken).
 
 Additions: ``iters`` (the reference fixes ITERS = 8 at build time) and
-``layout``: "rows" reads ``theta_pop`` (P, D) in ``es.unflatten``'s layout, as
-the reference does; "columns" reads ``theta_cols`` (D, P), the transpose, in
-which the 64 members of a wave load 256 contiguous bytes per weight.
+``schedule``:
+
+* "chunked" (default): the rollout runs in chunks of ``chunk_steps`` steps and
+  the survivors of each chunk (state, accumulators, weights) are packed into a
+  dense column buffer before the next. Episode lengths are heavy-tailed (mean
+  ~43 steps at the benchmark's shape while a few members last the whole
+  horizon), so this keeps waves full. It reads the weights as columns (D, P);
+  ``theta_pop`` given as (P, D) rows is transposed first (one copy), and
+  ``theta_cols`` skips that copy.
+* "rows": one member per lane for the whole rollout, ``theta_pop`` (P, D).
+* "columns": one member per lane, ``theta_cols`` (D, P), the transpose, in which
+  the 64 members of a wave load 256 contiguous bytes per weight.
+
+All three give identical results.
 """
 
 import torch
@@ -18,6 +29,8 @@ import torch
 from . import _lib
 
 LAYOUTS = {"rows": 0, "columns": 1}
+SCHEDULES = ("chunked", "rows", "columns")
+CHUNK_STEPS = 32
 SUPPORTED_C = (1, 2, 4)
 
 
@@ -27,12 +40,17 @@ def n_params(hidden, c):
 
 
 def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=0.0, height_gate=0.0, assist=0.0,
-            iters=8, layout="rows"):
-    """(fitness (P,), steps (P,)) float32 from state (2(3+C), P); asynchronous."""
+            iters=8, schedule="chunked", layout=None, theta_cols=None, chunk_steps=CHUNK_STEPS):
+    """(fitness (P,), steps (P,)) float32 from state (2(3+C), P); asynchronous.
+    ``theta_pop`` is (P, D) rows, or (D, P) for schedule "columns"; with schedule
+    "chunked" the columns may be given directly as ``theta_cols`` (then
+    ``theta_pop`` may be None). ``layout`` is the older name of ``schedule``."""
+    if layout is not None:
+        schedule = layout
     if int(c) not in SUPPORTED_C:
         raise ValueError(f"c must be one of {SUPPORTED_C}, got {c}")
-    if layout not in LAYOUTS:
-        raise ValueError(f"layout must be one of {tuple(LAYOUTS)}")
+    if schedule not in SCHEDULES:
+        raise ValueError(f"schedule must be one of {SCHEDULES}")
     if not 0 <= int(iters) <= 4096:
         raise ValueError("iters must be in [0, 4096]")
     c = int(c)
@@ -40,12 +58,25 @@ def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=
     hidden = _lib.check_hidden(hidden)
     horizon = _lib.check_horizon(horizon)
     d = n_params(hidden, c)
-    shape = (p, d) if layout == "rows" else (d, p)
-    theta_pop = _lib.check_theta(theta_pop, *shape, state.device)
+    if schedule == "chunked":
+        if theta_cols is None:
+            theta_cols = _lib.check_theta(theta_pop, p, d, state.device).T.contiguous()
+        theta_pop = _lib.check_theta(theta_cols, d, p, state.device, "theta_cols")
+    else:
+        shape = (d, p) if schedule == "columns" else (p, d)
+        theta_pop = _lib.check_theta(theta_pop, *shape, state.device)
     fitness = torch.empty(p, dtype=torch.float32, device=state.device)
     steps = torch.empty(p, dtype=torch.float32, device=state.device)
+    args = (float(alive_bonus), float(fall_penalty), float(height_gate), float(assist), _lib.ptr(fitness),
+            _lib.ptr(steps))
     with torch.cuda.device(state.device):
-        _lib.call("hipenvs_legged_es_rollout", c, hidden, int(iters), LAYOUTS[layout], _lib.ptr(state),
-                  _lib.ptr(theta_pop), p, horizon, float(alive_bonus), float(fall_penalty), float(height_gate),
-                  float(assist), _lib.ptr(fitness), _lib.ptr(steps), _lib.stream_of(state.device))
+        if schedule == "chunked":
+            nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=state.device)
+            _lib.call("hipenvs_legged_es_rollout_chunked", c, hidden, int(iters), int(chunk_steps), _lib.ptr(state),
+                      _lib.ptr(theta_pop), p, horizon, *args, _lib.ptr(workspace), nbytes,
+                      _lib.stream_of(state.device))
+        else:
+            _lib.call("hipenvs_legged_es_rollout", c, hidden, int(iters), LAYOUTS[schedule], _lib.ptr(state),
+                      _lib.ptr(theta_pop), p, horizon, *args, _lib.stream_of(state.device))
     return fitness, steps

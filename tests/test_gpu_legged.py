@@ -86,10 +86,35 @@ def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon):
     ef, es_ = olg.rollout_fused(state, theta, hidden, horizon, c)
     np.testing.assert_array_equal(to_np(fk), ef)
     np.testing.assert_array_equal(to_np(sk), es_)
-    fc, sc = legged_rollout.rollout(st, th.T.contiguous(), hidden, horizon, c, layout="columns")
+    fc, sc = legged_rollout.rollout(st, th.T.contiguous(), hidden, horizon, c, schedule="columns")
     np.testing.assert_array_equal(to_np(fc), ef)
     np.testing.assert_array_equal(to_np(sc), es_)
+    fr, sr = legged_rollout.rollout(st, th, hidden, horizon, c, schedule="rows")
+    np.testing.assert_array_equal(to_np(fr), ef)
+    np.testing.assert_array_equal(to_np(sr), es_)
     assert 1 <= es_.mean() <= horizon
+
+
+def test_chunked_schedule_at_scale_equals_static(dev):
+    """Populations larger than the resident grid (grid-stride loops), chunk lengths that do
+    and do not divide the horizon, and horizon 0 / 1: the compacting schedule equals the
+    one-member-per-lane kernel member for member."""
+    from hipenvs import legged, legged_rollout
+
+    c, hidden = 4, 16
+    for p, horizon, chunk in ((300_001, 70, 16), (300_001, 70, 32), (1000, 0, 32), (1000, 1, 32), (1, 30, 7),
+                              (4099, 200, 1)):
+        theta = torch.from_numpy(_population(p, c, hidden, 0.3, p % 97)).to(dev)
+        state = legged.Legged(c).reset(p, seed=3, device=dev)
+        fq, sq = legged_rollout.rollout(state, theta, hidden, horizon, c, schedule="chunked", chunk_steps=chunk)
+        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, schedule="rows")
+        assert torch.equal(fq, fs) and torch.equal(sq, ss), (p, horizon, chunk)
+    # assist keeps bodies up for the whole horizon: every member survives every chunk
+    theta = torch.from_numpy(_population(4096, c, hidden, 0.0, 1)).to(dev)
+    state = legged.Legged(c).reset(4096, seed=4, device=dev)
+    fq, sq = legged_rollout.rollout(state, theta, hidden, 100, c, assist=20.0, schedule="chunked", chunk_steps=16)
+    fs, ss = legged_rollout.rollout(state, theta, hidden, 100, c, assist=20.0, schedule="rows")
+    assert torch.equal(fq, fs) and torch.equal(sq, ss)
 
 
 def test_shaped_reward_and_assist_match_oracle(dev):

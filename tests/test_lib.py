@@ -33,8 +33,10 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_python_binding_covers_the_header():
     from hipenvs import _lib
 
-    status_fns = set(declared_functions()) - {"hipenvs_version", "hipenvs_last_hip_error"}
+    status_fns = set(declared_functions()) - {"hipenvs_version", "hipenvs_last_hip_error"} - set(_lib.VALUE_SIGNATURES)
     assert status_fns == set(_lib.SIGNATURES)
+    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(4, 64, 1000) > 1000 * 1676 * 4
+    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(3, 64, 1000) == -1
     assert _lib.version().startswith("hipenvs ")
     assert _lib.lib().hipenvs_last_hip_error() == 0
 
