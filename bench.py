@@ -57,6 +57,12 @@ HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3           # MI355X FP32 vector, packed (published)
 FP32_UNPACKED_TFLOPS = 78.6        # one FMA per lane per cycle
 CARTPOLE_BYTES = 41
+# HBM bytes per cartpole_step launch at N = 2**18: rocprofv3 --pmc FETCH_SIZE and then
+# WRITE_SIZE over `bench.py --only cartpole` read 2579.5 and 5376.0 KiB per dispatch;
+# the same counters read 131085.2 and 262144.0 KiB for a 256 MiB device copy in the same
+# process (--copy-mib 256), so they are scaled by 2.000 and 1.000. Commands and tables:
+# profiles/cartpole_step_n262144.md. Algorithmic bytes at this N: 41 x 2**18 = 10,747,904.
+CARTPOLE_TRAFFIC = {1 << 18: int(round((2579.5 * 262144.0 / 131085.2 + 5376.0 * 262144.0 / 262144.0) * 1024))}
 
 
 def log(msg):
@@ -79,6 +85,9 @@ def parse_args():
     p.add_argument("--legged-horizon", type=int, default=1000)
     p.add_argument("--sweep", action="store_true", help="also run the CartPole N = 2^0..2^24 sweep")
     p.add_argument("--sweep-out", default=None)
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="first run a plain device-to-device copy of this many MiB three times (a known-size "
+                        "kernel that scales hardware byte counters)")
     return p.parse_args()
 
 
@@ -207,6 +216,19 @@ def bench_cartpole(args, dev):
         f"array actions {fused['array_actions_env_steps_per_s']:,.0f} env-steps/s")
     del g, gk, gka, run
     return value, wall, launch, achieved, fused
+
+
+def bench_cartpole_at(n, steps, repeats, dev):
+    """The same single-step replay at another N (the 2**20 point of the step sweep)."""
+    run = CartPoleRun(n, steps, dev)
+    wall, ev = time_replay(run.graph_single(), repeats)
+    launch = ev / steps
+    gbs = CARTPOLE_BYTES * n / launch / 1e9
+    log(f"cartpole_step N={n}: {n * steps / wall:,.0f} env-steps/s; {launch * 1e6:.3f} us per launch -> {gbs:.1f} GB/s")
+    del run
+    return {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None}}
 
 
 def cpu_baseline_cartpole(n, seconds):
@@ -475,11 +497,21 @@ def main():
     dev = torch.device("cuda", 0)
     log(f"hipenvs: {_lib.version()} on {torch.cuda.get_device_name(dev)}; host os.cpu_count()={os.cpu_count()}")
     extra = {}
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.copy_mib} MiB x 3")
+        del src, dst
     value = wall = launch = achieved = None
     if args.only in (None, "cartpole"):
         value, wall, launch, achieved, fused = bench_cartpole(args, dev)
         extra["cartpole_fused_k32"] = fused
         extra["cartpole_step_us_per_launch"] = launch * 1e6
+        if args.n != 1 << 20:
+            extra["cartpole_step_n1048576"] = bench_cartpole_at(1 << 20, args.steps, args.repeats, dev)
         if args.sweep:
             extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out)
     if args.only in (None, "legged"):
@@ -516,9 +548,9 @@ def main():
         steps = args.legged_horizon
     else:
         roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": achieved / HBM_PEAK_GBS, "traffic": None}
+                    "frac": achieved / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(args.n)}
         config = {"workload": f"cartpole_step, N={args.n}, {args.steps} steps, one launch per step (HIP graph replay)",
-                  "n_envs": args.n, "parallelism": "single GPU, one thread per 4 envs"}
+                  "n_envs": args.n, "parallelism": "single GPU, one thread per env"}
         ms = wall * 1e3 / args.steps
         steps = args.steps
     line = {

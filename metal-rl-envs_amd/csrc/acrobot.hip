@@ -56,7 +56,9 @@ __device__ __forceinline__ S4 dsdt(const S4& s, float torque) {
   return S4{s.c, s.d, dd1, dd2};
 }
 
-__device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf((x + PI) / TWO_PI); }
+constexpr double INV_TWO_PI = 1.0 / (double)TWO_PI;  // for div_const(x, .) == x / TWO_PI
+
+__device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf(div_const(x + PI, INV_TWO_PI)); }
 
 // RK4 + wrap + clip in place (acrobot_np.py:47-61).
 __device__ __forceinline__ void rk4(S4& s, float torque) {

@@ -30,9 +30,12 @@ __device__ __forceinline__ uint32_t pcg_hash(uint32_t v) {
   return (w >> 22u) ^ w;
 }
 
-// float in [-bound, bound) from the top 24 bits of a hash (cartpole_metal.py:47-50).
+// float in [-bound, bound) from the top 24 bits of a hash (cartpole_metal.py:47-50):
+// ((h >> 8) * 2^-24 * 2 - 1) * bound. Every step before the last multiply is exact,
+// so the value is (m * 2^-23) * bound with m = (h >> 8) - 2^23 (|m| <= 2^23, exact in
+// float32), and m * (bound * 2^-23) rounds the same real number: one convert, one multiply.
 __device__ __forceinline__ float uniform_pm(uint32_t h, float bound) {
-  return ((float)(h >> 8) * (1.0f / 16777216.0f) * 2.0f - 1.0f) * bound;
+  return (float)((int32_t)(h >> 8) - 0x800000) * (bound * 0x1p-23f);
 }
 
 __device__ __forceinline__ uint32_t env_hash(uint32_t seed, uint32_t env) { return seed ^ (env * kGolden); }
@@ -135,6 +138,14 @@ __device__ __forceinline__ float det_tanh(float x) {
   const float t = e / (e + 2.0f);
   return copysignf(t, x);
 }
+
+// x / c for a float32 constant c, as one float64 product with inv_c = 1 / (double)c
+// rounded once to float32. The float64 product is within 2^-52 (relative) of x / c, and
+// a quotient of two float32 values never lies that close to a float32 rounding boundary
+// without being on it, which it cannot be; so this equals the IEEE float32 quotient for
+// every x, zeros, subnormals, infinities and NaN included. Each divisor used is also
+// checked against IEEE division over all 2^32 float32 inputs by the test suite.
+__device__ __forceinline__ float div_const(float x, double inv_c) { return (float)((double)x * inv_c); }
 
 // NaN-propagating clamp, numpy's np.clip semantics.
 __device__ __forceinline__ float clip(float v, float lo, float hi) {

@@ -30,7 +30,9 @@ constexpr float RESET_BOUND = 0x1.99999ap-4f; // float32(0.1)
 constexpr float TWO_PI = 0x1.921fb6p+2f;      // float32(2 * pi)
 constexpr float PI = 0x1.921fb6p+1f;          // float32(pi)
 
-__device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf((x + PI) / TWO_PI); }
+constexpr double INV_TWO_PI = 1.0 / (double)TWO_PI;  // for div_const(x, .) == x / TWO_PI
+
+__device__ __forceinline__ float wrap(float x) { return x - TWO_PI * floorf(div_const(x + PI, INV_TWO_PI)); }
 
 // Per-link loops are unrolled (U = K), so every per-link array is a set of
 // registers, except in the RK4 step past K = 16: its four chained evaluations no

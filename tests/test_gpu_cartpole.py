@@ -59,8 +59,8 @@ def test_sample_actions_and_reset_match_the_counter_rng(dev):
 
 @pytest.mark.parametrize("n", [1, 3, 100, 4096, 4099])
 def test_step_matches_oracle_on_random_states(dev, n):
-    """Random states in [-1, 1] (test_cartpole.py:33-37), both the dwordx4 path (n % 4 == 0)
-    and the scalar path; every column compared, terminal ones included."""
+    """Random states in [-1, 1] (test_cartpole.py:33-37), sizes on and off multiples of the
+    wave and block sizes; every column compared, terminal ones included."""
     from hipenvs import cartpole
 
     r = np.random.default_rng(n)
@@ -73,6 +73,37 @@ def test_step_matches_oracle_on_random_states(dev, n):
     assert_same_floats(to_np(rew), erew)
     np.testing.assert_array_equal(to_np(done), edone)
     assert ns.dtype == torch.float32 and rew.dtype == torch.float32 and done.dtype == torch.bool
+
+
+def assert_same_bits(got, expect):
+    """Bit-pattern equality, the sign of zero included; any NaN equals any NaN."""
+    got, expect = np.asarray(got, dtype=np.float32), np.asarray(expect, dtype=np.float32)
+    both_nan = np.isnan(got) & np.isnan(expect)
+    np.testing.assert_array_equal(np.where(both_nan, 0, got.view(np.uint32)),
+                                  np.where(both_nan, 0, expect.view(np.uint32)))
+
+
+def test_step_bit_exact_on_extreme_states(dev):
+    """Signed zeros, subnormals, huge angles (the float64 reduction), infinities and NaN in
+    every state row: the constant divisions, the sin/cos reduction and the termination test
+    agree with numpy's float32 arithmetic bit for bit, sign of zero included."""
+    from hipenvs import cartpole
+
+    specials = np.array([0.0, -0.0, 1e-40, -1e-40, 1e-45, 3e-39, 1e-20, -7e-12, 0.3, -2.0, 300.0, -1e5, 3.4e38,
+                         -3.4e38, np.inf, -np.inf, np.nan], dtype=np.float32)
+    r = np.random.default_rng(5)
+    n = 4096
+    state = r.choice(specials, size=(4, n)).astype(np.float32)
+    state[:, :64] = 0.0
+    state[2, :32] = -0.0
+    action = r.integers(0, 2, size=n).astype(np.int32)
+    cartpole.reseed(90)
+    ns, rew, done = cartpole.step(torch.from_numpy(state).to(dev), torch.from_numpy(action).to(dev))
+    with np.errstate(all="ignore"):
+        ens, erew, edone = oc.step(state, action, seed=91)
+    assert_same_bits(to_np(ns), ens)
+    assert_same_bits(to_np(rew), erew)
+    np.testing.assert_array_equal(to_np(done), edone)
 
 
 def test_terminal_fixture(dev):
