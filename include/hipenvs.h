@@ -214,6 +214,13 @@ int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, 
 int hipenvs_detmath(const float* x, float* sin_out, float* cos_out, float* tanh_out,
                     int64_t n, hipenvs_stream_t stream);
 
+/* Elementwise q = a / d (n) computed as the legged kernels divide by a shared divisor:
+ * through the float64 reciprocal of d, with an IEEE redo where that quotient came out
+ * subnormal (marked (n) u8 = 1 there). q must equal IEEE float32 a / d everywhere; used
+ * by the parity tests. */
+int hipenvs_div_recip(const float* a, const float* d, float* q, uint8_t* marked, int64_t n,
+                      hipenvs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -98,15 +98,17 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
   const float torque = (float)(action[i] - 1);
   rk4(s, torque);
   const bool d = terminal(s);
-  const uint32_t h = env_hash(seed, (uint32_t)i);
-  const float f0 = uniform_pm(pcg_hash(h), RESET_BOUND);
-  const float f1 = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
-  const float f2 = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
-  const float f3 = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
-  next[i] = d ? f0 : s.a;
-  next[n + i] = d ? f1 : s.b;
-  next[2 * n + i] = d ? f2 : s.c;
-  next[3 * n + i] = d ? f3 : s.d;
+  if (d) {  // fresh draws only on terminated lanes; the reference selects (acrobot_metal.py:76-80)
+    const uint32_t h = env_hash(seed, (uint32_t)i);
+    s.a = uniform_pm(pcg_hash(h), RESET_BOUND);
+    s.b = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
+    s.c = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
+    s.d = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
+  }
+  next[i] = s.a;
+  next[n + i] = s.b;
+  next[2 * n + i] = s.c;
+  next[3 * n + i] = s.d;
   reward[i] = d ? 0.0f : -1.0f;
   done[i] = d ? 1 : 0;
 }

@@ -44,16 +44,16 @@ __device__ __forceinline__ bool advance(float& x, float& xd, float& th, float& t
   return (fabsf(x) > X_LIMIT) || (fabsf(th) > THETA_LIMIT);
 }
 
-// Masked reset by select, every env computes the fresh state (cartpole_metal.py:86-93).
+// Masked reset (cartpole_metal.py:86-93): a terminated env takes four fresh draws. The
+// reference computes the draws for every env and selects; here they sit on the branch of
+// the terminated lanes, so a wave in which no env terminates skips the four hashes.
 __device__ __forceinline__ void reset_select(bool d, uint32_t h, float& x, float& xd, float& th, float& thd) {
-  const float f0 = uniform_pm(pcg_hash(h), RESET_BOUND);
-  const float f1 = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
-  const float f2 = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
-  const float f3 = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
-  x = d ? f0 : x;
-  xd = d ? f1 : xd;
-  th = d ? f2 : th;
-  thd = d ? f3 : thd;
+  if (d) {
+    x = uniform_pm(pcg_hash(h), RESET_BOUND);
+    xd = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
+    th = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
+    thd = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
+  }
 }
 
 // ---- kernels ---------------------------------------------------------------
@@ -119,17 +119,6 @@ __global__ __launch_bounds__(kBlock) void sample_actions_kernel(int32_t* __restr
   if (i >= n) return;
   const uint32_t h = env_hash(seed, (uint32_t)i);
   action[i] = (m == 2u) ? action_bit(h) : action_uniform(h, m);
-}
-
-__global__ __launch_bounds__(kBlock) void detmath_kernel(const float* __restrict__ x, float* __restrict__ s,
-                                                         float* __restrict__ c, float* __restrict__ th, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n) return;
-  float sv, cv;
-  det_sincos(x[i], &sv, &cv);
-  s[i] = sv;
-  c[i] = cv;
-  th[i] = det_tanh(x[i]);
 }
 
 // Fused ES rollout: one thread per member, the member's 7H+2 weights in
@@ -212,15 +201,6 @@ extern "C" int hipenvs_sample_actions(int32_t* action, int64_t n, int32_t m, uin
   if (n == 0) return HIPENVS_OK;
   hipLaunchKernelGGL(cp::sample_actions_kernel, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), action, n,
                      (uint32_t)m, seed);
-  return launch_status();
-}
-
-extern "C" int hipenvs_detmath(const float* x, float* sin_out, float* cos_out, float* tanh_out, int64_t n,
-                               hipenvs_stream_t stream) {
-  if (n < 0 || (n > 0 && (!x || !sin_out || !cos_out || !tanh_out))) return HIPENVS_E_ARG;
-  if (n == 0) return HIPENVS_OK;
-  hipLaunchKernelGGL(cp::detmath_kernel, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), x, sin_out, cos_out,
-                     tanh_out, n);
   return launch_status();
 }
 

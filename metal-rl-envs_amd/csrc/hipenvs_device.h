@@ -147,6 +147,38 @@ __device__ __forceinline__ float det_tanh(float x) {
 // checked against IEEE division over all 2^32 float32 inputs by the test suite.
 __device__ __forceinline__ float div_const(float x, double inv_c) { return (float)((double)x * inv_c); }
 
+// Division by a divisor used many times, through its correctly rounded float64 reciprocal
+// r = recip(d): q = RN32(RN64(a * r)). The float64 product is within 2^-52 (relative) of the
+// exact a / d. A quotient of two float32 values that is not itself a midpoint of the float32
+// grid lies at least 2^-49 (relative) from every midpoint (write a, d and the midpoint with
+// 24-, 24- and 25-bit significands, the midpoint's odd, and compare integer numerators),
+// and in the normal range it is never exactly on one. So q is the IEEE quotient whenever
+// that quotient is normal, zero, infinite or NaN (special operands pass through 1 / d and
+// the product as through IEEE division). Only a subnormal quotient can sit exactly on a
+// midpoint, where the product may round either way. DivRecip marks a lane whose quotient
+// came out nonzero subnormal (a compare and a select, no branch); its caller then redoes
+// the computation with IEEE division (DivIEEE), a path these bodies never take in practice.
+__device__ __forceinline__ double recip(float d) { return 1.0 / (double)d; }
+
+struct DivRecip {
+  // Per lane, the least (bits << 1) - 2 over the quotients, in uint32 arithmetic: the shift
+  // drops the sign, and the subtraction sends zero to the top, so a nonzero subnormal
+  // (0 < |bits| <= 0x7FFFFF) maps to at most 0xFFFFFC and every other value above it. One
+  // shift-add and one min per quotient, kept in a vector register.
+  uint32_t least = 0xFFFFFFFFu;
+  __device__ __forceinline__ float operator()(float a, float /*d*/, double r) {
+    const float q = (float)((double)a * r);
+    const uint32_t key = (__float_as_uint(q) << 1) - 2u;
+    least = key < least ? key : least;
+    return q;
+  }
+  __device__ __forceinline__ bool saw_subnormal() const { return least <= 0x00FFFFFCu; }
+};
+
+struct DivIEEE {
+  __device__ __forceinline__ float operator()(float a, float d, double /*r*/) const { return a / d; }
+};
+
 // NaN-propagating clamp, numpy's np.clip semantics.
 __device__ __forceinline__ float clip(float v, float lo, float hi) {
   v = (v < lo) ? lo : v;

@@ -40,18 +40,40 @@ __device__ __forceinline__ float max0(float x) { return (x < 0.0f) ? 0.0f : x; }
 
 // Exact impulse of one contact given its Delassus block and relative velocity
 // (hopper_np.py:80-109), float32 throughout.
-__device__ __forceinline__ void contact_impulse(float Att, float Atn, float Ann, float wt, float wn, float depth,
-                                                float& lt_out, float& ln_out) {
+// The per-substep constants of one contact's diagonal Delassus block: the 2x2 determinant
+// and the two cone-edge denominators with their float64 reciprocals, formed once per
+// substep instead of once per sweep (the values are the same float32 numbers either way).
+struct ContactBlock {
+  float Att, Atn, Ann, det, den_p, den_m;
+  double rdet, rden_p, rden_m;
+};
+
+__device__ __forceinline__ ContactBlock contact_block(float Att, float Atn, float Ann) {
+  ContactBlock b;
+  b.Att = Att;
+  b.Atn = Atn;
+  b.Ann = Ann;
+  b.det = Att * Ann - Atn * Atn;
+  b.den_p = Ann + MU * Atn;
+  b.den_m = Ann - MU * Atn;
+  b.rdet = recip(b.det);
+  b.rden_p = recip(b.den_p);
+  b.rden_m = recip(b.den_m);
+  return b;
+}
+
+template <class Div>
+__device__ __forceinline__ void contact_impulse(const ContactBlock& b, float wt, float wn, float depth,
+                                                float& lt_out, float& ln_out, Div& div) {
+  const float Att = b.Att, Atn = b.Atn, Ann = b.Ann;
   const bool touching = depth >= 0.0f;
   const float target = BAUMGARTE_OVER_H * max0(depth);
-  const float det = Att * Ann - Atn * Atn;
   const float tw = target - wn;
-  const float ln_stick = (Att * tw + Atn * wt) / det;
-  const float lt_stick = ((-Ann) * wt - Atn * tw) / det;
+  const float ln_stick = div(Att * tw + Atn * wt, b.det, b.rdet);
+  const float lt_stick = div((-Ann) * wt - Atn * tw, b.det, b.rdet);
   const bool sticks = fabsf(lt_stick) <= MU * ln_stick;
-  const float den_p = Ann + MU * Atn, den_m = Ann - MU * Atn;
-  const float ln_p = (den_p > 0.0f) ? max0(tw / den_p) : 0.0f;
-  const float ln_m = (den_m > 0.0f) ? max0(tw / den_m) : 0.0f;
+  const float ln_p = (b.den_p > 0.0f) ? max0(div(tw, b.den_p, b.rden_p)) : 0.0f;
+  const float ln_m = (b.den_m > 0.0f) ? max0(div(tw, b.den_m, b.rden_m)) : 0.0f;
   const float slip_p = wt + (Att * MU + Atn) * ln_p;
   const float s = (slip_p <= 0.0f) ? 1.0f : -1.0f;
   const float ln_slide = (slip_p <= 0.0f) ? ln_p : ln_m;
@@ -64,28 +86,29 @@ __device__ __forceinline__ void contact_impulse(float Att, float Atn, float Ann,
 }
 
 // Solve L L^T x = b in place (pendulum_np.py:95-107): forward then backward substitution.
-template <int N>
-__device__ __forceinline__ void chol_solve(const float (&L)[N][N], float (&b)[N]) {
+// rL[i] = recip(L[i][i]): the 2N divisions of a solve share the N diagonal reciprocals.
+template <int N, class Div>
+__device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double (&rL)[N], float (&b)[N], Div& div) {
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     float s = b[i];
 #pragma unroll
     for (int p = 0; p < i; ++p) s = s - L[i][p] * b[p];
-    b[i] = s / L[i][i];
+    b[i] = div(s, L[i][i], rL[i]);
   }
 #pragma unroll
   for (int i = N - 1; i >= 0; --i) {
     float s = b[i];
 #pragma unroll
     for (int p = i + 1; p < N; ++p) s = s - L[p][i] * b[p];
-    b[i] = s / L[i][i];
+    b[i] = div(s, L[i][i], rL[i]);
   }
 }
 
 // One semi-implicit Euler substep with block PGS contacts, in place (legged_np.py:57-97).
-template <int C>
+template <int C, class Div>
 __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
-                                        float assist, float assist_damping) {
+                                        float assist, float assist_damping, Div& div) {
   constexpr int N = 3 + C;
   float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
 #pragma unroll
@@ -138,7 +161,8 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     f[3 + j] = f[3 + j] + tq[j];
   }
   f[2] = (f[2] - assist * q[2]) - assist_damping * v[2];
-  // Cholesky in place (pendulum_np.py:88-94)
+  // Cholesky in place (pendulum_np.py:88-94), keeping each pivot's float64 reciprocal
+  double rL[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
 #pragma unroll
@@ -146,10 +170,15 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       float s = L[i][j];
 #pragma unroll
       for (int p = 0; p < j; ++p) s = s - L[i][p] * L[j][p];
-      L[i][j] = (i == j) ? sqrtf(s) : s / L[j][j];
+      if (i == j) {
+        L[i][i] = sqrtf(s);
+        rL[i] = recip(L[i][i]);
+      } else {
+        L[i][j] = div(s, L[j][j], rL[j]);
+      }
     }
   }
-  chol_solve<N>(L, f);
+  chol_solve<N>(L, rL, f, div);
   float vf[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) vf[i] = v[i] + H * f[i];
@@ -162,8 +191,8 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       MiJt[k][i] = (i == 0) ? 1.0f : (i == 2 || i == 3 + k) ? ca[k] : 0.0f;
       MiJn[k][i] = (i == 1) ? 1.0f : (i == 2 || i == 3 + k) ? sa[k] : 0.0f;
     }
-    chol_solve<N>(L, MiJt[k]);
-    chol_solve<N>(L, MiJn[k]);
+    chol_solve<N>(L, rL, MiJt[k], div);
+    chol_solve<N>(L, rL, MiJn[k], div);
   }
   // Delassus blocks A[k][l] = (Jt_k.MiJt_l, Jt_k.MiJn_l, Jn_k.MiJt_l, Jn_k.MiJn_l) and free velocities
   float Att[C][C], Atn[C][C], Ant[C][C], Ann[C][C], w0t[C], w0n[C];
@@ -181,10 +210,12 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
   }
   // block projected Gauss-Seidel, fixed contact order (legged_np.py:88-93)
   float lt[C], ln[C];
+  ContactBlock blk[C];
 #pragma unroll
   for (int k = 0; k < C; ++k) {
     lt[k] = 0.0f;
     ln[k] = 0.0f;
+    blk[k] = contact_block(Att[k][k], Atn[k][k], Ann[k][k]);
   }
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
@@ -202,7 +233,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       }
       const float wt = (C == 1) ? w0t[k] : w0t[k] + st;
       const float wn = (C == 1) ? w0n[k] : w0n[k] + sn;
-      contact_impulse(Att[k][k], Atn[k][k], Ann[k][k], wt, wn, depth[k], lt[k], ln[k]);
+      contact_impulse(blk[k], wt, wn, depth[k], lt[k], ln[k], div);
     }
   }
   // v = v_free + sum_k M^-1 J_k^T lambda_k; q += h v
@@ -217,6 +248,32 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
   }
 }
 
+// One substep dividing through the shared float64 reciprocals; a lane on which a quotient
+// came out subnormal (never met in practice) redoes the substep from its saved state with
+// IEEE division, so the result is always the IEEE one.
+template <int C>
+__device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
+                                              float assist, float assist_damping) {
+  constexpr int N = 3 + C;
+  float q0[N], v0[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q0[i] = q[i];
+    v0[i] = v[i];
+  }
+  DivRecip fast;
+  substep<C>(q, v, tq, iters, assist, assist_damping, fast);
+  if (fast.saw_subnormal()) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      q[i] = q0[i];
+      v[i] = v0[i];
+    }
+    DivIEEE ieee;
+    substep<C>(q, v, tq, iters, assist, assist_damping, ieee);
+  }
+}
+
 template <int C>
 __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
   return (q[1] < FALL_HEIGHT) || (fabsf(q[2]) > FALL_ANGLE);
@@ -227,6 +284,11 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
 // kernel's order (hidden unit j: bias, then the observations in order; head o:
 // bias, then the hidden units in order). POLICY_UNROLL hidden units per loop
 // iteration bounds how many of the member's weight loads are in flight at once.
+// Minimum resident waves per SIMD the rollout kernels are compiled for (bounds their VGPRs).
+#ifndef LEGGED_ROLLOUT_MIN_WAVES
+#define LEGGED_ROLLOUT_MIN_WAVES 1
+#endif
+
 #ifndef POLICY_UNROLL
 #define POLICY_UNROLL 2
 #endif
@@ -285,16 +347,22 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
     a /= 3;
   }
 #pragma unroll 1
-  for (int s = 0; s < SUBSTEPS; ++s) substep<C>(q, v, tq, iters, assist, assist_damping);
+  for (int s = 0; s < SUBSTEPS; ++s) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
   const bool d = fallen<C>(q);
-  const uint32_t h = env_hash(seed, (uint32_t)e);
-#pragma unroll
-  for (int i = 0; i < 2 * N; ++i) {
-    const float fresh = stand[i] + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
-    next[i * n + e] = d ? fresh : (i < N ? q[i] : v[i - N]);
-  }
   reward[e] = d ? 0.0f : v[0] + 1.0f;
   done[e] = d ? 1 : 0;
+  if (d) {  // fresh draws only on fallen lanes; the reference selects (legged_metal.py:148-152)
+    const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = stand[i] + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      v[i] = stand[N + i] + uniform_pm(pcg_hash(h + (uint32_t)(N + i) * kRowStride), RESET_BOUND);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) next[i * n + e] = q[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) next[(N + i) * n + e] = v[i];
 }
 
 template <int C>
@@ -312,7 +380,7 @@ __global__ __launch_bounds__(kBlock) void reset_kernel(const float* __restrict__
 // Fused ES rollout (legged_rollout_metal.py:19-59). Weight d of member i is
 // theta[i * D + d] (rows) or theta[d * p + i] (columns).
 template <int C, int HID, bool kColumns>
-__global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
+__global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
                                                      int64_t p, int32_t horizon, int iters, float alive, float fall,
                                                      float gate, float assist, float assist_damping,
                                                      float* __restrict__ fitness, float* __restrict__ steps_out) {
@@ -333,7 +401,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
   for (int32_t t = 0; t < horizon; ++t) {
     policy_torques<C, HID>(w, stride, q, v, tq);
 #pragma unroll 1
-    for (int s = 0; s < SUBSTEPS; ++s) substep<C>(q, v, tq, iters, assist, assist_damping);
+    for (int s = 0; s < SUBSTEPS; ++s) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
     if (fallen<C>(q)) {
       taken += 1.0f;
       total = total - fall;
@@ -369,7 +437,7 @@ struct Packed {
 };
 
 template <int C, int HID, bool kFirst>
-__global__ __launch_bounds__(64) void rollout_chunk_kernel(const float* __restrict__ state0,
+__global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_kernel(const float* __restrict__ state0,
                                                            const float* __restrict__ theta0, int64_t p,
                                                            Packed src, Packed dst, int64_t cap,
                                                            int32_t chunk_steps, int32_t horizon, int iters,
@@ -411,7 +479,7 @@ __global__ __launch_bounds__(64) void rollout_chunk_kernel(const float* __restri
       if (!live) continue;
       policy_torques<C, HID>(w, src_stride, q, v, tq);
 #pragma unroll 1
-      for (int sub = 0; sub < SUBSTEPS; ++sub) substep<C>(q, v, tq, iters, assist, assist_damping);
+      for (int sub = 0; sub < SUBSTEPS; ++sub) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
       ++t;
       bool finished;
       if (fallen<C>(q)) {

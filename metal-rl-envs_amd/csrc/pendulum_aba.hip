@@ -211,20 +211,23 @@ __device__ __forceinline__ void load(const float* __restrict__ state, int64_t n,
 
 // Masked reset: all 2K rows U[+-0.1] (RK4 task) or angles U[+-0.1] and zero velocities (Euler task),
 // row p of env e hashed at (seed ^ e*golden) + p * 0x85EBCA6B (pendulum_aba_metal.py:109-113).
+// The reference draws for every env and selects; the draws here sit on the terminated lanes'
+// branch, so a wave with no termination (the common case: K up to 2K hashes saved) skips them.
 template <int K, bool kZeroVelocity, int U = K>
-__device__ __forceinline__ void store_with_reset(float* __restrict__ next, int64_t n, int64_t e, const float* th,
-                                                 const float* om, bool d, uint32_t seed) {
-  const uint32_t h = env_hash(seed, (uint32_t)e);
+__device__ __forceinline__ void store_with_reset(float* __restrict__ next, int64_t n, int64_t e, float* th,
+                                                 float* om, bool d, uint32_t seed) {
+  if (d) {
+    const uint32_t h = env_hash(seed, (uint32_t)e);
 #pragma unroll U
-  for (int p = 0; p < K; ++p) {
-    const float fresh = uniform_pm(pcg_hash(h + (uint32_t)p * kRowStride), RESET_BOUND);
-    next[p * n + e] = d ? fresh : th[p];
+    for (int p = 0; p < K; ++p) th[p] = uniform_pm(pcg_hash(h + (uint32_t)p * kRowStride), RESET_BOUND);
+#pragma unroll U
+    for (int p = 0; p < K; ++p)
+      om[p] = kZeroVelocity ? 0.0f : uniform_pm(pcg_hash(h + (uint32_t)(K + p) * kRowStride), RESET_BOUND);
   }
 #pragma unroll U
-  for (int p = 0; p < K; ++p) {
-    const float fresh = kZeroVelocity ? 0.0f : uniform_pm(pcg_hash(h + (uint32_t)(K + p) * kRowStride), RESET_BOUND);
-    next[(K + p) * n + e] = d ? fresh : om[p];
-  }
+  for (int p = 0; p < K; ++p) next[p * n + e] = th[p];
+#pragma unroll U
+  for (int p = 0; p < K; ++p) next[(K + p) * n + e] = om[p];
 }
 
 template <int K>

@@ -31,6 +31,7 @@ SIGNATURES = {
     "hipenvs_cartpole_step_k": [_P, _P, _U32, _I32, _P, _P, _P, _I64, _P],
     "hipenvs_sample_actions": [_P, _I64, _I32, _U32, _P],
     "hipenvs_detmath": [_P, _P, _P, _P, _I64, _P],
+    "hipenvs_div_recip": [_P, _P, _P, _P, _I64, _P],
     "hipenvs_cartpole_es_rollout": [_P, _P, _I64, _I32, _I32, _P, _P],
     "hipenvs_acrobot_reset": [_P, _I64, _U32, _P],
     "hipenvs_acrobot_step": [_P, _P, _U32, _P, _P, _P, _I64, _P],

@@ -6,6 +6,12 @@
   the kernels pass to it is checked against IEEE division over all 2^32 float32 inputs
   by a small C program (``tests/csrc/div_const_check.c``), so the substitution cannot
   change a bit of any kernel output.
+* ``DivRecip`` (``hipenvs_device.h``) divides by a divisor used many times (the legged
+  body's Cholesky pivots, Delassus determinants and cone denominators) through its float64
+  reciprocal, and marks nonzero subnormal quotients for an IEEE redo;
+  ``tests/csrc/div_recip_check.c`` checks the marking key over all 2^32 bit patterns, the
+  quotient against IEEE division on random, special and near-midpoint operand pairs, and
+  that the exact subnormal midpoints it gets wrong are all marked.
 * ``uniform_pm`` evaluates ``((h >> 8) * 2^-24 * 2 - 1) * bound``
   (cartpole_metal.py:47-50) as ``((h >> 8) - 2^23) * (bound * 2^-23)``; checked here
   for all 2^24 values of ``h >> 8`` against the literal float32 expression.
@@ -76,6 +82,39 @@ def test_div_const_checker_catches_a_wrong_reciprocal(tmp_path):
                    check=True)
     out = subprocess.run([str(exe), "0x1.19999ap+0"], capture_output=True, text=True, timeout=600)
     assert out.returncode == 1 and "mismatches=0" not in out.stdout
+
+
+def _build(tmp_path, source_text, name):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / f"{name}.c"
+    src.write_text(source_text)
+    exe = tmp_path / name
+    subprocess.run([gcc, "-O2", "-fopenmp", "-ffp-contract=off", "-o", str(exe), str(src), "-lm"], check=True)
+    return exe
+
+
+DIV_RECIP_SRC = ROOT / "tests" / "csrc" / "div_recip_check.c"
+
+
+def test_div_recip_matches_ieee_except_marked_subnormals(tmp_path):
+    exe = _build(tmp_path, DIV_RECIP_SRC.read_text(), "div_recip_check")
+    out = subprocess.run([str(exe), "20000000"], capture_output=True, text=True, timeout=600)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "key_mismatches=0" in out.stdout and " mismatches=0" in out.stdout, out.stdout
+
+
+def test_div_recip_checker_catches_unmarked_subnormals(tmp_path):
+    """Not vacuous: taking the marked subnormal quotients as final answers fails it (the exact
+    subnormal midpoints come out wrong)."""
+    text = DIV_RECIP_SRC.read_text()
+    planted = text.replace("if (is_subnormal_nonzero(q)) { ++flagged; continue; }", "").replace(
+        "if (!is_subnormal_nonzero(q)) {", "if (1) {")
+    assert planted.count("is_subnormal_nonzero(q)") == text.count("is_subnormal_nonzero(q)") - 2
+    exe = _build(tmp_path, planted, "planted")
+    out = subprocess.run([str(exe), "20000000"], capture_output=True, text=True, timeout=600)
+    assert out.returncode == 1 and " mismatches=0" not in out.stdout, out.stdout
 
 
 @pytest.mark.parametrize("bound", [np.float32(0.05), np.float32(0.1), np.float32(1.0), np.float32(0.03),
