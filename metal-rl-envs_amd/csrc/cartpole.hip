@@ -72,18 +72,28 @@ __global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state
 // One env per thread, any n and alignment. At every batch size this beats packing four
 // envs per thread into 16-byte accesses (2.96 vs 3.81 us at N = 2^18, 7.9 vs 9.3 us at
 // 2^20): a step is short, and the extra waves hide more of the load latency.
+// The four reset draws depend only on the seed and the env index, so they are computed
+// for every env (as the reference's select does) while its state loads are in flight;
+// the empty asm marks the draws as needed there, which keeps the compiler from sinking
+// them past the physics, where they would add to the step's latency instead.
 __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ state, const int32_t* __restrict__ action,
                                                       uint32_t seed, float* __restrict__ next, float* __restrict__ reward,
                                                       uint8_t* __restrict__ done, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= n) return;
   float x = state[i], xd = state[n + i], th = state[2 * n + i], thd = state[3 * n + i];
-  const bool d = advance(x, xd, th, thd, action[i]);
-  reset_select(d, env_hash(seed, (uint32_t)i), x, xd, th, thd);
-  next[i] = x;
-  next[n + i] = xd;
-  next[2 * n + i] = th;
-  next[3 * n + i] = thd;
+  const int32_t a = action[i];
+  const uint32_t h = env_hash(seed, (uint32_t)i);
+  float f0 = uniform_pm(pcg_hash(h), RESET_BOUND);
+  float f1 = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
+  float f2 = uniform_pm(pcg_hash(h + kRowOff2), RESET_BOUND);
+  float f3 = uniform_pm(pcg_hash(h + kRowOff3), RESET_BOUND);
+  asm volatile("" : "+v"(f0), "+v"(f1), "+v"(f2), "+v"(f3));
+  const bool d = advance(x, xd, th, thd, a);
+  next[i] = d ? f0 : x;
+  next[n + i] = d ? f1 : xd;
+  next[2 * n + i] = d ? f2 : th;
+  next[3 * n + i] = d ? f3 : thd;
   reward[i] = 1.0f;
   done[i] = d ? 1 : 0;
 }

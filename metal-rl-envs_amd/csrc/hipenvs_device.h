@@ -78,13 +78,14 @@ constexpr float TANH_CLAMP = 10.0f;
 }  // namespace dm
 
 __device__ __forceinline__ void det_sincos(float x, float* sin_out, float* cos_out) {
-  float r;
-  int q;
-  if (fabsf(x) <= dm::SMALL_ARG) {
-    const float k = rintf(x * dm::TWO_OVER_PI);
-    r = (((x - k * dm::PIO2_1) - k * dm::PIO2_2) - k * dm::PIO2_3) - k * dm::PIO2_4;
-    q = (int)k & 3;
-  } else {
+  // float32 reduction, computed for every lane on an argument clamped into its range (so
+  // no branch precedes it and independent work can overlap the loads that feed x) ...
+  const bool small = fabsf(x) <= dm::SMALL_ARG;
+  const float xs = small ? x : 0.0f;
+  const float k = rintf(xs * dm::TWO_OVER_PI);
+  float r = (((xs - k * dm::PIO2_1) - k * dm::PIO2_2) - k * dm::PIO2_3) - k * dm::PIO2_4;
+  int q = (int)k & 3;
+  if (!small) {  // ... and the float64 reduction for |x| > 256, inf and NaN
     const double xd = (double)x;
     const double kd = rint(xd * dm::TWO_OVER_PI_D);
     r = (float)((xd - kd * dm::PIO2_1D) - kd * dm::PIO2_2D);
