@@ -279,24 +279,51 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
   return (q[1] < FALL_HEIGHT) || (fabsf(q[2]) > FALL_ANGLE);
 }
 
-// The member's (5+2C)-HID-3C tanh policy and per-leg torques (legged_rollout_metal.py:217-236).
-// Weight d of the member is w[d * stride]. Every accumulator sums in the reference
-// kernel's order (hidden unit j: bias, then the observations in order; head o:
-// bias, then the hidden units in order). POLICY_UNROLL hidden units per loop
-// iteration bounds how many of the member's weight loads are in flight at once.
 // Minimum resident waves per SIMD the rollout kernels are compiled for (bounds their VGPRs).
 #ifndef LEGGED_ROLLOUT_MIN_WAVES
 #define LEGGED_ROLLOUT_MIN_WAVES 1
 #endif
 
+// POLICY_UNROLL hidden units per policy loop iteration bounds how many of the member's
+// weight loads are in flight at once.
 #ifndef POLICY_UNROLL
-#define POLICY_UNROLL 2
+#define POLICY_UNROLL 4
 #endif
-template <int C, int HID>
-__device__ __forceinline__ void policy_torques(const float* __restrict__ w, int64_t stride, const float (&q)[3 + C],
-                                               const float (&v)[3 + C], float (&tq)[C]) {
+
+// Rows of the policy weights. FlatRows is es.unflatten's layout (es.py:152-164): w1 (OBS, HID)
+// row-major, b1 (HID), w2 (HID, OUT) row-major, b2 (OUT), the layout callers pass in.
+// UnitRows is the compacted sets' layout: hidden unit j's bias, its OBS input weights and
+// its OUT head weights on 1 + OBS + OUT consecutive rows, then b2; a unit's rows then lie
+// within one immediate-offset range of a single address (26 rows of 256 B at C = 4).
+template <int OBS, int HID, int OUT>
+struct FlatRows {
+  static constexpr int w1(int i, int j) { return i * HID + j; }
+  static constexpr int b1(int j) { return OBS * HID + j; }
+  static constexpr int w2(int j, int o) { return OBS * HID + HID + j * OUT + o; }
+  static constexpr int b2(int o) { return OBS * HID + HID + HID * OUT + o; }
+};
+
+template <int OBS, int HID, int OUT>
+struct UnitRows {
+  static constexpr int kUnit = 1 + OBS + OUT;
+  static constexpr int b1(int j) { return j * kUnit; }
+  static constexpr int w1(int i, int j) { return j * kUnit + 1 + i; }
+  static constexpr int w2(int j, int o) { return j * kUnit + 1 + OBS + o; }
+  static constexpr int b2(int o) { return HID * kUnit + o; }
+};
+
+// The member's (5+2C)-HID-3C tanh policy and per-leg torques (legged_rollout_metal.py:217-236).
+// Every accumulator sums in the reference kernel's order (hidden unit j: bias, then the
+// observations in order; head o: bias, then the hidden units in order).
+// Weight row r of the member is w[r * stride]; Rows maps each weight to its row. kStride > 0
+// fixes the stride at compile time (the compacted sets' 64-member tiles), so neighbouring
+// rows are immediate offsets from one address instead of one 64-bit address add per load.
+template <int C, int HID, template <int, int, int> class Rows = FlatRows, int kStride = 0>
+__device__ __forceinline__ void policy_torques(const float* __restrict__ w, int64_t runtime_stride,
+                                               const float (&q)[3 + C], const float (&v)[3 + C], float (&tq)[C]) {
+  const int64_t stride = kStride > 0 ? (int64_t)kStride : runtime_stride;
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
-  constexpr int B1 = OBS * HID, W2 = B1 + HID, B2 = W2 + HID * OUT;
+  using R = Rows<OBS, HID, OUT>;
   float obs[OBS];
 #pragma unroll
   for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
@@ -304,15 +331,15 @@ __device__ __forceinline__ void policy_torques(const float* __restrict__ w, int6
   for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
   float logit[OUT];
 #pragma unroll
-  for (int o = 0; o < OUT; ++o) logit[o] = w[(B2 + o) * stride];
+  for (int o = 0; o < OUT; ++o) logit[o] = w[R::b2(o) * stride];
 #pragma unroll POLICY_UNROLL
   for (int j = 0; j < HID; ++j) {
-    float s = w[(B1 + j) * stride];
+    float s = w[R::b1(j) * stride];
 #pragma unroll
-    for (int k = 0; k < OBS; ++k) s = s + obs[k] * w[(k * HID + j) * stride];
+    for (int k = 0; k < OBS; ++k) s = s + obs[k] * w[R::w1(k, j) * stride];
     const float hj = det_tanh(s);
 #pragma unroll
-    for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w[(W2 + j * OUT + o) * stride];
+    for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w[R::w2(j, o) * stride];
   }
 #pragma unroll
   for (int leg = 0; leg < C; ++leg) {
@@ -386,7 +413,6 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_kernel(c
                                                      float* __restrict__ fitness, float* __restrict__ steps_out) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
-  constexpr int B1 = OBS * HID, W2 = B1 + HID, B2 = W2 + HID * OUT;
   const int64_t e = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (e >= p) return;
   const float* w = kColumns ? theta + e : theta + e * D;
@@ -428,13 +454,21 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_kernel(c
 // host round trip. Every loop is bounded (a member runs at most `horizon`
 // steps, a chunk at most `chunk_steps`), and each member's arithmetic is the
 // same as in the one-member-per-lane kernel, whatever slot it lands in.
+// A compacted member set. cap is a multiple of 64; the weights are stored in tiles of 64
+// members, tile t holding (D, 64) columns: weight d of slot s at
+// (s / 64) * D * 64 + d * 64 + s % 64, so a wave (one tile) reads weight d of its 64
+// members as one coalesced 256-byte row at a compile-time stride.
 struct Packed {
   float* state;      // (2N, cap): q then v
-  float* theta;      // (D, cap)
+  float* theta;      // (cap / 64) tiles of (D, 64)
   float* acc;        // (2, cap): total, taken
   int32_t* meta;     // (2, cap): member id, steps done
   uint32_t* count;
 };
+
+constexpr int kTile = 64;
+
+__host__ __device__ constexpr int64_t round_to_tile(int64_t n) { return (n + kTile - 1) / kTile * kTile; }
 
 template <int C, int HID, bool kFirst>
 __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_kernel(const float* __restrict__ state0,
@@ -446,10 +480,9 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_ke
                                                            float* __restrict__ steps_out) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
-  constexpr int B1 = OBS * HID, W2 = B1 + HID, B2 = W2 + HID * OUT;
   const unsigned lane = threadIdx.x;
   const int64_t count = kFirst ? p : (int64_t)*src.count;
-  const int64_t src_stride = kFirst ? p : cap;
+  const int64_t src_stride = kFirst ? p : cap;  // state rows; the weights use tiles after the first chunk
   const float* sstate = kFirst ? state0 : src.state;
   const float* stheta = kFirst ? theta0 : src.theta;
   for (int64_t base = (int64_t)blockIdx.x * 64; base < count; base += (int64_t)gridDim.x * 64) {
@@ -473,11 +506,16 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_ke
         t = src.meta[cap + i];
       }
     }
-    const float* w = stheta + i;
+    // the caller's (D, p) columns in the first chunk; the set's tile of this wave after
+    const float* w = kFirst ? stheta + i : stheta + (base / kTile) * (int64_t)D * kTile + lane;
     for (int32_t k = 0; k < chunk_steps; ++k) {
       if (!__any(live)) break;
       if (!live) continue;
-      policy_torques<C, HID>(w, src_stride, q, v, tq);
+      if constexpr (kFirst) {
+        policy_torques<C, HID>(w, src_stride, q, v, tq);
+      } else {
+        policy_torques<C, HID, UnitRows, kTile>(w, kTile, q, v, tq);
+      }
 #pragma unroll 1
       for (int sub = 0; sub < SUBSTEPS; ++sub) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
       ++t;
@@ -515,7 +553,19 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_ke
         dst.acc[cap + slot] = taken;
         dst.meta[slot] = id;
         dst.meta[cap + slot] = t;
-        for (int d = 0; d < D; ++d) dst.theta[d * cap + slot] = w[d * src_stride];
+        float* wd = dst.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
+        if constexpr (kFirst) {  // caller's FlatRows columns -> UnitRows tile
+          using F = FlatRows<OBS, HID, OUT>;
+          using T = UnitRows<OBS, HID, OUT>;
+          for (int j = 0; j < HID; ++j) {
+            wd[T::b1(j) * kTile] = w[F::b1(j) * src_stride];
+            for (int k = 0; k < OBS; ++k) wd[T::w1(k, j) * kTile] = w[F::w1(k, j) * src_stride];
+            for (int o = 0; o < OUT; ++o) wd[T::w2(j, o) * kTile] = w[F::w2(j, o) * src_stride];
+          }
+          for (int o = 0; o < OUT; ++o) wd[T::b2(o) * kTile] = w[F::b2(o) * src_stride];
+        } else {  // tile -> tile, same rows
+          for (int d = 0; d < D; ++d) wd[d * kTile] = w[d * kTile];
+        }
       }
     }
   }
@@ -529,7 +579,7 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
                    float* steps, void* workspace, hipStream_t s) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
-  const int64_t cap = p;
+  const int64_t cap = round_to_tile(p);
   // carve the workspace: two packed sets, then two counters
   char* ws = static_cast<char*>(workspace);
   Packed set[2];
@@ -686,7 +736,7 @@ extern "C" int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t 
     return -1;
   const int64_t n = 3 + c, obs = 5 + 2 * c, out = 3 * c;
   const int64_t d = obs * hidden + hidden + hidden * out + out;
-  return 2 * (2 * n + d + 4) * p * 4 + 64;
+  return 2 * (2 * n + d + 4) * lg::round_to_tile(p) * 4 + 64;
 }
 
 extern "C" int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
