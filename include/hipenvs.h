@@ -189,8 +189,9 @@ int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iters, int32_t 
                               hipenvs_stream_t stream);
 
 /* Bytes of device workspace hipenvs_legged_es_rollout_chunked needs for p
- * members: two packed member sets (state, weights, accumulators, ids) and two
- * counters; -1 for an unsupported c or hidden. */
+ * members: two packed member sets of p rounded up to 64 slots (state, weights in
+ * 64-member tiles, accumulators, ids) and two counters; -1 for an unsupported c
+ * or hidden. */
 int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t hidden, int64_t p);
 
 /* The same rollout, scheduled in chunks of `chunk_steps` steps: after each
