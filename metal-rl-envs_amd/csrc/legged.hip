@@ -106,9 +106,17 @@ __device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double 
 }
 
 // One semi-implicit Euler substep with block PGS contacts, in place (legged_np.py:57-97).
-template <int C, class Div>
+// kGroup = 0: one lane computes the whole substep. kGroup = G > 0: the G lanes g = 0..G-1 of
+// a member's group all hold the member's state and compute everything identically, except
+// the 2C + 1 triangular solves: lane g < 2C + 1 solves right-hand side g (the forces, then
+// the tangent, then the normal Jacobian rows) and the results are exchanged through the
+// group's LDS rows xs ((2C + 1) x 8 floats). Every value is computed by the same expression
+// as in the one-lane form, so the results are the same bits. Callers keep the group's
+// lanes in one single-wave workgroup, so the barriers order its LDS traffic.
+template <int C, class Div, int kGroup = 0>
 __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
-                                        float assist, float assist_damping, Div& div) {
+                                        float assist, float assist_damping, Div& div, float* xs = nullptr,
+                                        int g = 0) {
   constexpr int N = 3 + C;
   float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
 #pragma unroll
@@ -178,22 +186,61 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       }
     }
   }
-  chol_solve<N>(L, rL, f, div);
+  // M^-1 f and the M^-1 J^T columns
+  float MiJt[C][N], MiJn[C][N];
+  if constexpr (kGroup == 0) {
+    chol_solve<N>(L, rL, f, div);
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        MiJt[k][i] = (i == 0) ? 1.0f : (i == 2 || i == 3 + k) ? ca[k] : 0.0f;
+        MiJn[k][i] = (i == 1) ? 1.0f : (i == 2 || i == 3 + k) ? sa[k] : 0.0f;
+      }
+      chol_solve<N>(L, rL, MiJt[k], div);
+      chol_solve<N>(L, rL, MiJn[k], div);
+    }
+  } else {
+    static_assert(kGroup >= 2 * C + 1, "one lane per right-hand side");
+    constexpr int kRow = 8;  // LDS floats per right-hand side
+    const int rhs = g < 2 * C + 1 ? g : 0;  // lanes past 2C solve the forces again, unused
+    const bool normal = rhs > C;
+    const int k = normal ? rhs - 1 - C : rhs - 1;
+    float ck = ca[0], sk = sa[0];
+#pragma unroll
+    for (int kk = 1; kk < C; ++kk) {
+      ck = (k == kk) ? ca[kk] : ck;
+      sk = (k == kk) ? sa[kk] : sk;
+    }
+    float b[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const bool on = (i == 2 || i == 3 + k);
+      const float jt = (i == 0) ? 1.0f : on ? ck : 0.0f;
+      const float jn = (i == 1) ? 1.0f : on ? sk : 0.0f;
+      b[i] = (rhs == 0) ? f[i] : normal ? jn : jt;
+    }
+    chol_solve<N>(L, rL, b, div);
+    __syncthreads();  // the rows' previous readers are done
+    if (g < 2 * C + 1) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) xs[g * kRow + i] = b[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) f[i] = xs[i];
+#pragma unroll
+    for (int kk = 0; kk < C; ++kk) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        MiJt[kk][i] = xs[(1 + kk) * kRow + i];
+        MiJn[kk][i] = xs[(1 + C + kk) * kRow + i];
+      }
+    }
+  }
   float vf[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) vf[i] = v[i] + H * f[i];
-  // M^-1 J^T columns
-  float MiJt[C][N], MiJn[C][N];
-#pragma unroll
-  for (int k = 0; k < C; ++k) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      MiJt[k][i] = (i == 0) ? 1.0f : (i == 2 || i == 3 + k) ? ca[k] : 0.0f;
-      MiJn[k][i] = (i == 1) ? 1.0f : (i == 2 || i == 3 + k) ? sa[k] : 0.0f;
-    }
-    chol_solve<N>(L, rL, MiJt[k], div);
-    chol_solve<N>(L, rL, MiJn[k], div);
-  }
   // Delassus blocks A[k][l] = (Jt_k.MiJt_l, Jt_k.MiJn_l, Jn_k.MiJt_l, Jn_k.MiJn_l) and free velocities
   float Att[C][C], Atn[C][C], Ant[C][C], Ann[C][C], w0t[C], w0n[C];
 #pragma unroll
@@ -274,6 +321,33 @@ __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + 
   }
 }
 
+// The group form of substep_exact: the fast divisions, and when any live lane of the wave saw
+// a subnormal quotient the whole wave redoes the substep with IEEE division (identical bits
+// wherever nothing was marked), which keeps the group's barriers in uniform control flow.
+template <int C, int G>
+__device__ __forceinline__ void substep_exact_group(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C],
+                                                    int iters, float assist, float assist_damping, float* xs, int g,
+                                                    bool live) {
+  constexpr int N = 3 + C;
+  float q0[N], v0[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q0[i] = q[i];
+    v0[i] = v[i];
+  }
+  DivRecip fast;
+  substep<C, DivRecip, G>(q, v, tq, iters, assist, assist_damping, fast, xs, g);
+  if (__any(live && fast.saw_subnormal())) {  // lanes of finished members step on, unused
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      q[i] = q0[i];
+      v[i] = v0[i];
+    }
+    DivIEEE ieee;
+    substep<C, DivIEEE, G>(q, v, tq, iters, assist, assist_damping, ieee, xs, g);
+  }
+}
+
 template <int C>
 __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
   return (q[1] < FALL_HEIGHT) || (fabsf(q[2]) > FALL_ANGLE);
@@ -346,6 +420,52 @@ __device__ __forceinline__ void policy_torques(const float* __restrict__ w, int6
     float torque = -1.0f, best = logit[3 * leg];
     if (logit[3 * leg + 1] > best) { torque = 0.0f; best = logit[3 * leg + 1]; }
     if (logit[3 * leg + 2] > best) { torque = 1.0f; }
+    tq[leg] = torque * TORQUE;
+  }
+}
+
+// The group form of policy_torques for a compacted member (UnitRows tile, stride 64): lane g
+// of the G-lane group computes hidden units g, g + G, ...; lane o < 3C sums head o over all
+// hidden units in order; the group exchanges the hidden values and the logits through its
+// LDS rows xh (HID floats) and xl (3C floats). Sums in the same order as policy_torques.
+template <int C, int HID, int G>
+__device__ __forceinline__ void policy_group(const float* __restrict__ w, const float (&q)[3 + C],
+                                             const float (&v)[3 + C], float (&tq)[C], float* xh, float* xl, int g) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  static_assert(G >= OUT, "one lane per head");
+  using R = UnitRows<OBS, HID, OUT>;
+  constexpr int64_t kStride = 64;
+  float obs[OBS];
+#pragma unroll
+  for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
+#pragma unroll
+  for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
+  float hs[(HID + G - 1) / G];
+#pragma unroll
+  for (int u = 0; u < (HID + G - 1) / G; ++u) {
+    const int j = g + G * u < HID ? g + G * u : 0;  // lanes past HID recompute unit 0, unused
+    float sj = w[R::b1(j) * kStride];
+#pragma unroll
+    for (int k = 0; k < OBS; ++k) sj = sj + obs[k] * w[R::w1(k, j) * kStride];
+    hs[u] = det_tanh(sj);
+  }
+  __syncthreads();  // the rows' previous readers are done
+#pragma unroll
+  for (int u = 0; u < (HID + G - 1) / G; ++u)
+    if (g + G * u < HID) xh[g + G * u] = hs[u];
+  __syncthreads();
+  if (g < OUT) {
+    float lo = w[R::b2(g) * kStride];
+#pragma unroll 8
+    for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w[R::w2(j, g) * kStride];
+    xl[g] = lo;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int leg = 0; leg < C; ++leg) {
+    float torque = -1.0f, best = xl[3 * leg];
+    if (xl[3 * leg + 1] > best) { torque = 0.0f; best = xl[3 * leg + 1]; }
+    if (xl[3 * leg + 2] > best) { torque = 1.0f; }
     tq[leg] = torque * TORQUE;
   }
 }
@@ -470,6 +590,87 @@ constexpr int kTile = 64;
 
 __host__ __device__ constexpr int64_t round_to_tile(int64_t n) { return (n + kTile - 1) / kTile * kTile; }
 
+// The tail of a rollout: once at most wide_max members survive (about one wave per SIMD in
+// this form), each compacted member gets a group of kGroupLanes lanes and runs to the end
+// of its episode (policy_group, substep_exact_group), kGroupMembers members per wave. The
+// group shortens one member's step, which is what bounds the tail. Results are those of the
+// one-lane schedule, bit for bit.
+constexpr int kGroupLanes = 16;
+constexpr int kGroupMembers = 64 / kGroupLanes;
+
+template <int C, int HID>
+__device__ __forceinline__ void rollout_group_tail(const Packed& src, int64_t count, int64_t cap, int32_t horizon,
+                                                   int iters, float alive_bonus, float fall, float gate,
+                                                   float assist, float assist_damping, float* __restrict__ fitness,
+                                                   float* __restrict__ steps_out, float* xs_all, float* xh_all,
+                                                   float* xl_all) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  constexpr int G = kGroupLanes, M = kGroupMembers;
+  const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
+  float* xs = xs_all + mloc * (2 * C + 1) * 8;
+  float* xh = xh_all + mloc * HID;
+  float* xl = xl_all + mloc * 16;
+  for (int64_t mbase = (int64_t)blockIdx.x * M; mbase < count; mbase += (int64_t)gridDim.x * M) {
+    const int64_t i = mbase + mloc;
+    bool live = i < count;
+    const int64_t slot = live ? i : mbase;  // a lane group past the count steps slot mbase, unused
+    float q[N], v[N], tq[C];
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      q[r] = src.state[r * cap + slot];
+      v[r] = src.state[(N + r) * cap + slot];
+    }
+    float total = src.acc[slot], taken = src.acc[cap + slot];
+    const int32_t id = src.meta[slot];
+    int32_t t = src.meta[cap + slot];
+    const float* w = src.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
+    while (__any(live)) {  // every lane steps, so the groups' barriers stay uniform
+      policy_group<C, HID, G>(w, q, v, tq, xh, xl, g);
+#pragma unroll 1
+      for (int sub = 0; sub < SUBSTEPS; ++sub)
+        substep_exact_group<C, G>(q, v, tq, iters, assist, assist_damping, xs, g, live);
+      if (live) {
+        ++t;
+        bool finished;
+        if (fallen<C>(q)) {
+          taken += 1.0f;
+          total = total - fall;
+          finished = true;
+        } else {
+          total = total + (((q[1] >= gate) ? v[0] : 0.0f) + alive_bonus);
+          taken += 1.0f;
+          finished = t >= horizon;
+        }
+        if (finished) {
+          if (g == 0) {
+            fitness[id] = total;
+            steps_out[id] = taken;
+          }
+          live = false;
+        }
+      }
+    }
+  }
+}
+
+// The group tail as a kernel of its own, launched after every later chunk: it runs when the
+// set holds at most wide_max members and exits at once otherwise (rollout_chunk_kernel does
+// the opposite). Kept apart so that the one-lane kernel's code is compiled on its own.
+template <int C, int HID>
+__global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t cap, int32_t horizon, int iters,
+                                                          float alive_bonus, float fall, float gate, float assist,
+                                                          float assist_damping, float* __restrict__ fitness,
+                                                          float* __restrict__ steps_out, int64_t wide_max) {
+  const int64_t count = (int64_t)*src.count;
+  if (count > wide_max) return;
+  __shared__ float xs_all[kGroupMembers * (2 * C + 1) * 8];
+  __shared__ float xh_all[kGroupMembers * HID];
+  __shared__ float xl_all[kGroupMembers * 16];
+  rollout_group_tail<C, HID>(src, count, cap, horizon, iters, alive_bonus, fall, gate, assist, assist_damping, fitness,
+                             steps_out, xs_all, xh_all, xl_all);
+}
+
 template <int C, int HID, bool kFirst>
 __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_kernel(const float* __restrict__ state0,
                                                            const float* __restrict__ theta0, int64_t p,
@@ -477,11 +678,12 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_ke
                                                            int32_t chunk_steps, int32_t horizon, int iters,
                                                            float alive_bonus, float fall, float gate, float assist,
                                                            float assist_damping, float* __restrict__ fitness,
-                                                           float* __restrict__ steps_out) {
+                                                           float* __restrict__ steps_out, int64_t wide_max) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
   const unsigned lane = threadIdx.x;
   const int64_t count = kFirst ? p : (int64_t)*src.count;
+  if (!kFirst && count <= wide_max) return;  // rollout_tail_kernel takes the set (the same count everywhere)
   const int64_t src_stride = kFirst ? p : cap;  // state rows; the weights use tiles after the first chunk
   const float* sstate = kFirst ? state0 : src.state;
   const float* stheta = kFirst ? theta0 : src.theta;
@@ -606,17 +808,25 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   const float af = (float)assist, ad = (float)(0.1 * assist);
   // first chunk: the caller's arrays -> set 0
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
+  // the group tail takes over once the survivors fit kGroupMembers to a wave at one wave per SIMD
+  const int64_t wide_max = (int64_t)kGroupMembers * 4 * cus;
   hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true>), dim3((unsigned)needed), dim3(64), 0, s, state, theta_cols,
-                     p, set[1], set[0], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps);
+                     p, set[1], set[0], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
+                     wide_max);
   int status = launch_status();
   int cur = 0;
   const int64_t grid = resident < needed ? resident : needed;
+  // one member group per workgroup: the tail never holds more than min(p, wide_max) members
+  const int64_t tail_members = p < wide_max ? p : wide_max;
+  const int64_t tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
   for (int64_t done = chunk_steps; status == HIPENVS_OK && done < horizon; done += chunk_steps) {
     const int nxt = 1 - cur;
     hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[nxt].count, 0u);
     hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state, theta_cols,
                        p, set[cur], set[nxt], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness,
-                       steps);
+                       steps, wide_max);
+    hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)tail_grid), dim3(64), 0, s, set[cur], cap,
+                       horizon, iters, alive, fall, gate, af, ad, fitness, steps, wide_max);
     status = launch_status();
     cur = nxt;
   }
