@@ -596,6 +596,9 @@ __host__ __device__ constexpr int64_t round_to_tile(int64_t n) { return (n + kTi
 // group shortens one member's step, which is what bounds the tail. Results are those of the
 // one-lane schedule, bit for bit.
 constexpr int kGroupLanes = 16;
+#ifndef LEGGED_TAIL_MEMBERS_PER_CU
+#define LEGGED_TAIL_MEMBERS_PER_CU 16  // survivors per CU at the switch: one 4-member wave per SIMD
+#endif
 constexpr int kGroupMembers = 64 / kGroupLanes;
 
 template <int C, int HID>
@@ -809,7 +812,7 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   // first chunk: the caller's arrays -> set 0
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
   // the group tail takes over once the survivors fit kGroupMembers to a wave at one wave per SIMD
-  const int64_t wide_max = (int64_t)kGroupMembers * 4 * cus;
+  const int64_t wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * cus;
   hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true>), dim3((unsigned)needed), dim3(64), 0, s, state, theta_cols,
                      p, set[1], set[0], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
                      wide_max);

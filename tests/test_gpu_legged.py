@@ -117,6 +117,26 @@ def test_chunked_schedule_at_scale_equals_static(dev):
     assert torch.equal(fq, fs) and torch.equal(sq, ss)
 
 
+@pytest.mark.parametrize("c,hidden", [(1, 4), (1, 64), (2, 8), (2, 32), (4, 4), (4, 64)])
+def test_group_tail_equals_static(dev, c, hidden):
+    """Populations that the compacting schedule hands to its group tail (a lane group per
+    member) after the first chunk, at every leg count and hidden width the group code
+    distinguishes (one to four hidden units per lane, 2C + 1 solve lanes, 3C head lanes),
+    with assisted members that stay up for the whole horizon: member for member equal to
+    the one-member-per-lane kernel."""
+    from hipenvs import legged, legged_rollout
+
+    p, horizon = 3001, 150
+    theta = torch.from_numpy(_population(p, c, hidden, 0.3, 11 * c + hidden)).to(dev)
+    state = legged.Legged(c).reset(p, seed=5, device=dev)
+    for assist in (0.0, 20.0):
+        fq, sq = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="chunked",
+                                        chunk_steps=8)
+        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="rows")
+        assert torch.equal(fq, fs) and torch.equal(sq, ss), (c, hidden, assist)
+        assert ss.max().item() > 8  # members outlived the first chunk
+
+
 def test_shaped_reward_and_assist_match_oracle(dev):
     """test_es.py:71-104's variants: alive 0.1 + fall penalty 20 (some fitness negative),
     and the assist spring with a gate."""
