@@ -156,9 +156,95 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
   steps_out[i] = steps;
 }
 
+// The same rollout with a group of kRolloutLanes lanes per member (four members to a
+// single-wave workgroup), for populations that would fill only a fraction of the SIMDs with
+// one member per lane: lane g computes hidden units g, g + 16, ... from the weights it holds;
+// lanes 0..2 sum the three heads over all hidden values, read in order from the group's LDS
+// row; observation and RK4 physics run identically on all 16 lanes. Same bits as the one-lane
+// form.
+constexpr int kRolloutLanes = 16;
+constexpr int kRolloutMembers = 64 / kRolloutLanes;
+
+template <int H>
+__global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restrict__ state,
+                                                           const float* __restrict__ theta, int64_t p,
+                                                           int32_t horizon, float* __restrict__ steps_out) {
+  constexpr int D = 10 * H + 3, G = kRolloutLanes, U = (H + G - 1) / G;
+  __shared__ float xh_all[kRolloutMembers * H];
+  __shared__ float xl_all[kRolloutMembers * 4];
+  const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
+  float* xh = xh_all + mloc * H;
+  float* xl = xl_all + mloc * 4;
+  const int64_t i = (int64_t)blockIdx.x * kRolloutMembers + mloc;
+  bool alive = i < p;
+  const int64_t m = alive ? i : p - 1;  // a group past p steps member p - 1, unused
+  const float* row = theta + m * D;
+  float w1[U][6], b1[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = g + G * u < H ? g + G * u : 0;  // lanes past H recompute unit 0, unused
+#pragma unroll
+    for (int k = 0; k < 6; ++k) w1[u][k] = row[k * H + j];
+    b1[u] = row[6 * H + j];
+  }
+  const int o = g < 3 ? g : 0;
+  float w2[H];
+#pragma unroll
+  for (int j = 0; j < H; ++j) w2[j] = row[7 * H + 3 * j + o];
+  const float b2 = row[10 * H + o];
+  S4 s{state[m], state[p + m], state[2 * p + m], state[3 * p + m]};
+  float steps = 0.0f;
+  int32_t t = 0;
+  alive = alive && horizon > 0;
+  while (__any(alive)) {  // every lane steps, so the barriers stay uniform
+    float ob[6];
+    det_sincos(s.a, &ob[1], &ob[0]);
+    det_sincos(s.b, &ob[3], &ob[2]);
+    ob[4] = s.c;
+    ob[5] = s.d;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float pre = ob[0] * w1[u][0];
+#pragma unroll
+      for (int k = 1; k < 6; ++k) pre = pre + ob[k] * w1[u][k];
+      const float h = det_tanh(pre + b1[u]);
+      if (g + G * u < H) xh[g + G * u] = h;
+    }
+    __syncthreads();
+    if (g < 3) {
+      float l = b2;
+#pragma unroll
+      for (int j = 0; j < H; ++j) l = l + xh[j] * w2[j];
+      xl[g] = l;
+    }
+    __syncthreads();
+    const float l0 = xl[0], l1 = xl[1], l2 = xl[2];
+    __syncthreads();  // the group's rows are read before the next step writes them
+    float torque = -1.0f, best = l0;
+    if (l1 > best) { torque = 0.0f; best = l1; }
+    if (l2 > best) { torque = 1.0f; }
+    rk4(s, torque);
+    const bool done = terminal(s);
+    if (alive) {
+      if (done) {
+        alive = false;
+      } else {
+        steps += 1.0f;
+        alive = ++t < horizon;
+      }
+    }
+  }
+  if (g == 0 && i < p) steps_out[i] = steps;
+}
+
 template <int H>
 int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+  if (p <= group_rollout_limit()) {
+    hipLaunchKernelGGL(rollout_group_kernel<H>, dim3((unsigned)((p + kRolloutMembers - 1) / kRolloutMembers)),
+                       dim3(64), 0, s, state, theta, p, horizon, out);
+  } else {
+    hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+  }
   return launch_status();
 }
 

@@ -163,9 +163,84 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
   fitness[i] = survived;
 }
 
+// The same rollout with a group of kRolloutLanes lanes per member (four members to a
+// single-wave workgroup), for populations that would fill only a fraction of the SIMDs with
+// one member per lane: lane g computes hidden units g, g + 16, ... from the weights it holds;
+// lanes 0 and 1 sum the two heads over all hidden values, read in order from the group's LDS
+// row; the physics runs identically on all 16 lanes. A member's step then costs about a
+// quarter of the one-lane form's instruction latency, and the results are the same bits.
+constexpr int kRolloutLanes = 16;
+constexpr int kRolloutMembers = 64 / kRolloutLanes;
+
+template <int H>
+__global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restrict__ state,
+                                                           const float* __restrict__ theta, int64_t p,
+                                                           int32_t horizon, float* __restrict__ fitness) {
+  constexpr int D = 7 * H + 2, G = kRolloutLanes, U = (H + G - 1) / G;
+  __shared__ float xh_all[kRolloutMembers * H];
+  __shared__ float xl_all[kRolloutMembers * 2];
+  const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
+  float* xh = xh_all + mloc * H;
+  float* xl = xl_all + mloc * 2;
+  const int64_t i = (int64_t)blockIdx.x * kRolloutMembers + mloc;
+  bool alive = i < p;
+  const int64_t m = alive ? i : p - 1;  // a group past p steps member p - 1, unused
+  const float* row = theta + m * D;
+  float w1[U][4], b1[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = g + G * u < H ? g + G * u : 0;  // lanes past H recompute unit 0, unused
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w1[u][k] = row[k * H + j];
+    b1[u] = row[4 * H + j];
+  }
+  const int o = g < 2 ? g : 0;
+  float w2[H];
+#pragma unroll
+  for (int j = 0; j < H; ++j) w2[j] = row[5 * H + 2 * j + o];
+  const float b2 = row[7 * H + o];
+  float x = state[m], xd = state[p + m], th = state[2 * p + m], thd = state[3 * p + m];
+  float survived = 0.0f;
+  int32_t t = 0;
+  alive = alive && horizon > 0;
+  while (__any(alive)) {  // every lane steps, so the barriers stay uniform
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float pre = (((x * w1[u][0] + xd * w1[u][1]) + th * w1[u][2]) + thd * w1[u][3]) + b1[u];
+      const float h = det_tanh(pre);
+      if (g + G * u < H) xh[g + G * u] = h;
+    }
+    __syncthreads();
+    if (g < 2) {
+      float l = b2;
+#pragma unroll
+      for (int j = 0; j < H; ++j) l = l + xh[j] * w2[j];
+      xl[g] = l;
+    }
+    __syncthreads();
+    const float l0 = xl[0], l1 = xl[1];
+    __syncthreads();  // the group's rows are read before the next step writes them
+    const bool done = advance(x, xd, th, thd, (l1 > l0) ? 1 : 0);
+    if (alive) {
+      if (done) {
+        alive = false;
+      } else {
+        survived += 1.0f;
+        alive = ++t < horizon;
+      }
+    }
+  }
+  if (g == 0 && i < p) fitness[i] = survived;
+}
+
 template <int H>
 int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+  if (p <= group_rollout_limit()) {
+    hipLaunchKernelGGL(rollout_group_kernel<H>, dim3((unsigned)((p + kRolloutMembers - 1) / kRolloutMembers)),
+                       dim3(64), 0, s, state, theta, p, horizon, out);
+  } else {
+    hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+  }
   return launch_status();
 }
 

@@ -191,6 +191,16 @@ __device__ __forceinline__ float clip(float v, float lo, float hi) {
 // ---------------------------------------------------------------------------
 constexpr int kBlock = 256;
 
+// Populations up to this size run the fused ES rollouts with a lane group per member: 16
+// members per CU, i.e. one four-member wave per SIMD. 0 when the device cannot be queried.
+inline int64_t group_rollout_limit() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess)
+    return 0;
+  return 16 * (int64_t)cus;
+}
+
 inline unsigned grid_for(int64_t items, int block = kBlock) {
   return (unsigned)((items + block - 1) / block);
 }

@@ -32,7 +32,7 @@ def population(p, d, seed, scale=None, sigma=0.1):
     return (theta0[None, :] + np.float32(sigma) * eps).astype(np.float32)
 
 
-@pytest.mark.parametrize("hidden", [4, 16, 32])
+@pytest.mark.parametrize("hidden", [4, 8, 16, 32, 64])
 def test_cartpole_rollout_matches_oracle(dev, hidden):
     from hipenvs import cartpole_rollout
 
@@ -43,7 +43,7 @@ def test_cartpole_rollout_matches_oracle(dev, hidden):
     np.testing.assert_array_equal(to_np(got), oc.rollout_survived(state, theta, hidden, horizon))
 
 
-@pytest.mark.parametrize("hidden", [4, 16, 32])
+@pytest.mark.parametrize("hidden", [4, 8, 16, 32, 64])
 def test_acrobot_rollout_matches_oracle(dev, hidden):
     from hipenvs import acrobot_rollout
 
@@ -52,6 +52,23 @@ def test_acrobot_rollout_matches_oracle(dev, hidden):
     state = oa.reset(p, seed=4)
     got = acrobot_rollout.rollout_steps(torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev), hidden, horizon)
     np.testing.assert_array_equal(to_np(got), oa.rollout_steps(state, theta, hidden, horizon))
+
+
+@pytest.mark.parametrize("hidden", [8, 32])
+def test_large_populations_one_member_per_lane(dev, hidden):
+    """Populations above the lane-group limit (16 members per CU) run one member per lane;
+    both bodies, bit for bit against the oracle."""
+    from hipenvs import acrobot_rollout, cartpole_rollout
+
+    p = 20_000
+    theta = population(p, 7 * hidden + 2, 100 + hidden, scale=0.5)
+    state = oc.reset(p, seed=5)
+    got = cartpole_rollout.rollout_steps(torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev), hidden, 150)
+    np.testing.assert_array_equal(to_np(got), oc.rollout_survived(state, theta, hidden, 150))
+    theta = population(p, 10 * hidden + 3, 200 + hidden, scale=0.5)
+    state = oa.reset(p, seed=6)
+    got = acrobot_rollout.rollout_steps(torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev), hidden, 60)
+    np.testing.assert_array_equal(to_np(got), oa.rollout_steps(state, theta, hidden, 60))
 
 
 def test_config2_cartpole_population(dev):
