@@ -250,7 +250,27 @@ def cpu_baseline_cartpole(n, seconds):
     return n * steps / el, steps
 
 
-def sweep(dev, steps0, k, out_path):
+def cpu_rate_cartpole(n, seconds):
+    """numpy CartPole env-steps/s at N (the oracle's step with np.sin/np.cos, one process)."""
+    from oracle import cartpole as oc
+    from oracle import rng
+
+    state = oc.reset(n, seed=0)
+    actions = [rng.action_bits(t, n) for t in range(1, 5)]
+    state, _, _ = oc.step(state, actions[0], seed=1, trig="numpy")
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        state, _, _ = oc.step(state, actions[steps % 4], seed=steps + 2, trig="numpy")
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return n * steps / el
+
+
+def sweep(dev, steps0, k, out_path, cpu_seconds=0.25):
+    """Config-1 sweep: single-step and K-fused rates at N = 2^0..2^20 (and 2^22, 2^24), with the
+    numpy rate at each N unless cpu_seconds is 0; the crossover is the first N where the
+    single-step GPU rate passes numpy's."""
     rows = []
     for e in list(range(0, 21)) + [22, 24]:
         n = 1 << e
@@ -262,14 +282,17 @@ def sweep(dev, steps0, k, out_path):
         launch = ev1 / steps
         row = dict(n=n, steps=steps, single=n * steps / w1, fused_inkernel=n * steps / wk, fused_array=n * steps / wka,
                    launch_us=launch * 1e6, single_gbs=CARTPOLE_BYTES * n / launch / 1e9)
+        if cpu_seconds > 0:
+            row["numpy"] = cpu_rate_cartpole(n, cpu_seconds)
         rows.append(row)
         log(f"N=2^{e:<2d} single {row['single']:>16,.0f}  fused(in-kernel) {row['fused_inkernel']:>16,.0f}  "
             f"fused(array) {row['fused_array']:>16,.0f} env-steps/s  launch {row['launch_us']:7.2f} us "
-            f"{row['single_gbs']:8.1f} GB/s")
+            f"{row['single_gbs']:8.1f} GB/s" + (f"  numpy {row['numpy']:>14,.0f}" if "numpy" in row else ""))
         del run
+    crossover = next((r["n"] for r in rows if "numpy" in r and r["single"] > r["numpy"]), None)
     if out_path:
-        Path(out_path).write_text(json.dumps(rows, indent=1))
-    return rows
+        Path(out_path).write_text(json.dumps({"rows": rows, "crossover_n": crossover}, indent=1))
+    return {"rows": rows, "crossover_n": crossover}
 
 
 # ---------------------------------------------------------------------------
@@ -513,7 +536,8 @@ def main():
         if args.n != 1 << 20:
             extra["cartpole_step_n1048576"] = bench_cartpole_at(1 << 20, args.steps, args.repeats, dev)
         if args.sweep:
-            extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out)
+            extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out,
+                                            0.0 if args.skip_cpu else 0.25)
     if args.only in (None, "legged"):
         legged = bench_legged(args, dev)
         if not args.skip_cpu:
