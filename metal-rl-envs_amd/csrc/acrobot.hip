@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= n) return;
   S4 s{state[i], state[n + i], state[2 * n + i], state[3 * n + i]};
-  const float torque = (float)(action[i] - 1);
+  const float torque = (float)(stream_load(action + i) - 1);
   rk4(s, torque);
   const bool d = terminal(s);
   if (d) {  // fresh draws only on terminated lanes; the reference selects (acrobot_metal.py:76-80)
@@ -109,8 +109,8 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
   next[n + i] = s.b;
   next[2 * n + i] = s.c;
   next[3 * n + i] = s.d;
-  reward[i] = d ? 0.0f : -1.0f;
-  done[i] = d ? 1 : 0;
+  stream_store(d ? 0.0f : -1.0f, reward + i);
+  stream_store((uint8_t)(d ? 1 : 0), done + i);
 }
 
 // Fused ES rollout: one thread per member, the member's 10H+3 weights in

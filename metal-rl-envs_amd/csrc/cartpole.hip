@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= n) return;
   float x = state[i], xd = state[n + i], th = state[2 * n + i], thd = state[3 * n + i];
-  const int32_t a = action[i];
+  const int32_t a = stream_load(action + i);
   const uint32_t h = env_hash(seed, (uint32_t)i);
   float f0 = uniform_pm(pcg_hash(h), RESET_BOUND);
   float f1 = uniform_pm(pcg_hash(h + kRowOff1), RESET_BOUND);
@@ -94,8 +94,8 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
   next[n + i] = d ? f1 : xd;
   next[2 * n + i] = d ? f2 : th;
   next[3 * n + i] = d ? f3 : thd;
-  reward[i] = 1.0f;
-  done[i] = d ? 1 : 0;
+  stream_store(1.0f, reward + i);
+  stream_store((uint8_t)(d ? 1 : 0), done + i);
 }
 
 // k chained steps, one env per thread (any n): rewards and dones written per step as
@@ -111,11 +111,11 @@ __global__ __launch_bounds__(kBlock) void step_k_kernel(const float* __restrict_
   float x = state[i], xd = state[n + i], th = state[2 * n + i], thd = state[3 * n + i];
   for (int32_t t = 0; t < k; ++t) {
     const uint32_t h = env_hash(seed + (uint32_t)t, (uint32_t)i);
-    const int32_t a = kArrayActions ? actions[(int64_t)t * n + i] : action_bit(h);
+    const int32_t a = kArrayActions ? stream_load(actions + (int64_t)t * n + i) : action_bit(h);
     const bool d = advance(x, xd, th, thd, a);
     reset_select(d, h, x, xd, th, thd);
-    rewards[(int64_t)t * n + i] = 1.0f;
-    dones[(int64_t)t * n + i] = d ? 1 : 0;
+    stream_store(1.0f, rewards + (int64_t)t * n + i);
+    stream_store((uint8_t)(d ? 1 : 0), dones + (int64_t)t * n + i);
   }
   next[i] = x;
   next[n + i] = xd;

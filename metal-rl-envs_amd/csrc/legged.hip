@@ -487,7 +487,7 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
     v[i] = state[(N + i) * n + e];
   }
   // leg k gets ((a / 3^k) % 3 - 1) * TORQUE (legged_np.py:51-54)
-  int32_t a = action[e];
+  int32_t a = stream_load(action + e);
 #pragma unroll
   for (int k = 0; k < C; ++k) {
     tq[k] = (float)(a % 3 - 1) * TORQUE;
@@ -496,8 +496,8 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
 #pragma unroll 1
   for (int s = 0; s < SUBSTEPS; ++s) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
   const bool d = fallen<C>(q);
-  reward[e] = d ? 0.0f : v[0] + 1.0f;
-  done[e] = d ? 1 : 0;
+  stream_store(d ? 0.0f : v[0] + 1.0f, reward + e);
+  stream_store((uint8_t)(d ? 1 : 0), done + e);
   if (d) {  // fresh draws only on fallen lanes; the reference selects (legged_metal.py:148-152)
     const uint32_t h = env_hash(seed, (uint32_t)e);
 #pragma unroll

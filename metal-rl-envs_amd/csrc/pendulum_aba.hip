@@ -240,11 +240,11 @@ __global__ __launch_bounds__(kBlock) void step_rk4_kernel(const float* __restric
   constexpr int U = K <= 16 ? K : 1;
   float th[K], om[K];
   load<K, U>(state, n, e, th, om);
-  rk4<K, U>(th, om, (float)(action[e] - 1) * 1.0f);
+  rk4<K, U>(th, om, (float)(stream_load(action + e) - 1) * 1.0f);
   const bool d = terminal<K, U>(th);
   store_with_reset<K, false, U>(next, n, e, th, om, d, seed);
-  reward[e] = d ? 0.0f : -1.0f;
-  done[e] = d ? 1 : 0;
+  stream_store(d ? 0.0f : -1.0f, reward + e);
+  stream_store((uint8_t)(d ? 1 : 0), done + e);
 }
 
 template <int K, bool kArrayTorque>
@@ -256,13 +256,13 @@ __global__ __launch_bounds__(kBlock) void step_euler_kernel(const float* __restr
   if (e >= n) return;
   float th[K], om[K];
   load<K>(state, n, e, th, om);
-  const float tq = kArrayTorque ? torque[e]
+  const float tq = kArrayTorque ? stream_load(torque + e)
                                 : uniform_pm(pcg_hash(env_hash(seed, (uint32_t)e) + kTorqueOffset), 1.0f);
   euler<K>(th, om, tq);
   const bool d = terminal<K>(th);
   store_with_reset<K, true>(next, n, e, th, om, d, seed);
-  reward[e] = d ? 0.0f : -1.0f;
-  done[e] = d ? 1 : 0;
+  stream_store(d ? 0.0f : -1.0f, reward + e);
+  stream_store((uint8_t)(d ? 1 : 0), done + e);
 }
 
 template <int K>
