@@ -57,12 +57,14 @@ HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3           # MI355X FP32 vector, packed (published)
 FP32_UNPACKED_TFLOPS = 78.6        # one FMA per lane per cycle
 CARTPOLE_BYTES = 41
-# HBM bytes per cartpole_step launch at N = 2**18: rocprofv3 --pmc FETCH_SIZE and then
-# WRITE_SIZE over `bench.py --only cartpole` read 2579.5 and 5376.0 KiB per dispatch;
-# the same counters read 131085.2 and 262144.0 KiB for a 256 MiB device copy in the same
-# process (--copy-mib 256), so they are scaled by 2.000 and 1.000. Commands and tables:
-# profiles/cartpole_step_n262144.md. Algorithmic bytes at this N: 41 x 2**18 = 10,747,904.
-CARTPOLE_TRAFFIC = {1 << 18: int(round((2579.5 * 262144.0 / 131085.2 + 5376.0 * 262144.0 / 262144.0) * 1024))}
+# HBM bytes per cartpole_step launch: rocprofv3 --pmc FETCH_SIZE and then WRITE_SIZE over
+# `bench.py --only cartpole --copy-mib 256` read 2579.5 / 5378.5 KiB per dispatch at N = 2**18
+# and 10259.6 / 21692.4 KiB at N = 2**20; the same counters read 131085.2 and 262144.0 KiB
+# for the 256 MiB device copy in the same process, so they are scaled by 2.000 and 1.000.
+# Commands and tables: profiles/cartpole_step_n262144.md. Algorithmic bytes: 41 x N.
+_FETCH_SCALE = 262144.0 / 131085.2
+CARTPOLE_TRAFFIC = {n: int(round((fetch * _FETCH_SCALE + write) * 1024))
+                    for n, fetch, write in ((1 << 18, 2579.5, 5378.5), (1 << 20, 10259.6, 21692.4))}
 
 
 def log(msg):
@@ -228,7 +230,7 @@ def bench_cartpole_at(n, steps, repeats, dev):
     del run
     return {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gbs / HBM_PEAK_GBS, "traffic": None}}
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(n)}}
 
 
 def cpu_baseline_cartpole(n, seconds):
