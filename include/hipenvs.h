@@ -208,6 +208,62 @@ int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, 
                                       float* fitness, float* steps, void* workspace, int64_t workspace_bytes,
                                       hipenvs_stream_t stream);
 
+/* ---- Seeded ES generation ---------------------------------------------- */
+/* The reference's generation (es.py:218-227) draws half = (P/2, D) normals,
+ * materialises eps = [half; -half] and theta + sigma * eps, and reduces
+ * sum(ranks[:, None] * eps, 0) / (P * sigma). These entry points replace those
+ * lines with noise regenerated from a counter RNG: member pair m has key
+ * pcg(seed ^ pcg(m + 0x6A09E667)); weight pair j is Box-Muller on
+ * h1 = pcg(key + 2j * 0x9E3779B9), h2 = pcg(key + (2j+1) * 0x9E3779B9) at
+ * 24-bit fixed point (ln, sin, cos in float32 elementary operations), giving
+ * eps[2j] = r cos, eps[2j+1] = r sin; member m + P/2 carries -eps[m].
+ * p is even, 2 <= p < 2^31; sigma and lr are rounded to float32 as numpy
+ * rounds Python scalars against float32 arrays. */
+
+/* The population theta (d) + sigma * [eps; -eps] for p members into out:
+ * layout 0 rows (p, d), layout 1 columns (d, p).
+ * Replaces `theta[None, :] + cfg.sigma * eps` with its noise draw (es.py:219-222). */
+int hipenvs_es_perturb(const float* theta, int64_t d, int64_t p, uint32_t seed, double sigma, int32_t layout,
+                       float* out, hipenvs_stream_t stream);
+
+/* Bytes of device workspace hipenvs_es_update needs (-1 for an unsupported shape). */
+int64_t hipenvs_es_update_workspace_bytes(int64_t d, int64_t p);
+
+/* theta_out (d) = theta + f32(lr) * (S / f32(p * sigma)), S[k] = sum over member pairs of
+ * (ranks[m] - ranks[m + p/2]) * eps[m][k]: float32 partial sums over chunks of
+ * 64 * ceil(p/2 / 16384) pairs in member order, then the partials in chunk order.
+ * ranks (p) f32 are the centered ranks of the fitness. theta_out may alias theta.
+ * Replaces the gradient and update lines of es.py:224-226. */
+int hipenvs_es_update(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed, double sigma,
+                      double lr, float* theta_out, void* workspace, int64_t workspace_bytes,
+                      hipenvs_stream_t stream);
+
+/* hipenvs_cartpole_es_rollout on the population of hipenvs_es_perturb (rows),
+ * which is written to workspace (workspace_bytes >= 4 * p * (7*hidden+2)) and
+ * never returned. Identical results to perturbing and rolling out separately.
+ * Replaces MetalBackend.rollout of a materialised population
+ * (es.py:222, es.py:263-267, cartpole_rollout_metal.py:88-100). */
+int hipenvs_cartpole_es_rollout_seeded(const float* state, const float* theta, int64_t p, uint32_t seed,
+                                       double sigma, int32_t hidden, int32_t horizon, float* fitness,
+                                       void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream);
+
+/* The same for Acrobot (workspace_bytes >= 4 * p * (10*hidden+3));
+ * acrobot_rollout_metal.py:69-81. */
+int hipenvs_acrobot_es_rollout_seeded(const float* state, const float* theta, int64_t p, uint32_t seed,
+                                      double sigma, int32_t hidden, int32_t horizon, float* steps,
+                                      void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream);
+
+/* hipenvs_legged_es_rollout_chunked on the population of hipenvs_es_perturb, whose
+ * weights are generated straight into the packed member tiles of the workspace
+ * (same size: hipenvs_legged_es_rollout_workspace_bytes), so no (p, D) array
+ * exists. Identical results to the chunked rollout of the perturbed columns.
+ * legged_rollout_metal.py:70-83 with es.py:218-222. */
+int hipenvs_legged_es_rollout_seeded(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
+                                     const float* state, const float* theta, int64_t p, uint32_t seed,
+                                     double sigma, int32_t horizon, float alive_bonus, float fall_penalty,
+                                     float height_gate, double assist, float* fitness, float* steps,
+                                     void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream);
+
 /* ---- Diagnostics (no reference counterpart) ---------------------------- */
 
 /* Elementwise deterministic sin, cos, tanh of x (n) as the kernels compute them;

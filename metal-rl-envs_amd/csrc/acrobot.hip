@@ -9,7 +9,7 @@
 // counter RNG of acrobot_metal.py:78-83. Per env-step the step kernel moves 41
 // algorithmic bytes; it is VALU-bound (14 sin/cos, 18 IEEE divisions).
 
-#include "hipenvs_device.h"
+#include "es_noise.h"
 
 namespace hipenvs {
 namespace ac {
@@ -282,4 +282,18 @@ extern "C" int hipenvs_acrobot_es_rollout(const float* state, const float* theta
     case 64: return ac::launch_rollout<64>(state, theta, p, horizon, steps, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
+}
+
+extern "C" int hipenvs_acrobot_es_rollout_seeded(const float* state, const float* theta, int64_t p, uint32_t seed,
+                                                 double sigma, int32_t hidden, int32_t horizon, float* steps,
+                                                 void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream) {
+  if (p < 2 || (p & 1) || p > 0x7fffffffLL || horizon < 0 || !state || !theta || !steps || !workspace)
+    return HIPENVS_E_ARG;
+  if (hidden != 4 && hidden != 8 && hidden != 16 && hidden != 32 && hidden != 64) return HIPENVS_E_UNSUPPORTED;
+  const int64_t d = 10 * (int64_t)hidden + 3;
+  if (workspace_bytes < (int64_t)sizeof(float) * p * d) return HIPENVS_E_ARG;
+  float* population = static_cast<float*>(workspace);  // (p, d) rows, written here, read by the rollout
+  const int status = launch_perturb(theta, d, p, seed, (float)sigma, kPerturbRows, population, as_stream(stream));
+  if (status != HIPENVS_OK) return status;
+  return hipenvs_acrobot_es_rollout(state, population, p, hidden, horizon, steps, stream);
 }

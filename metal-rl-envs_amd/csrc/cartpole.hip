@@ -9,7 +9,7 @@
 // moves 41 algorithmic bytes: 16 B state in, 4 B action, 16 B state out,
 // 4 B reward, 1 B done.
 
-#include "hipenvs_device.h"
+#include "es_noise.h"
 
 namespace hipenvs {
 namespace cp {
@@ -302,4 +302,18 @@ extern "C" int hipenvs_cartpole_es_rollout(const float* state, const float* thet
     case 64: return cp::launch_rollout<64>(state, theta, p, horizon, fitness, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
+}
+
+extern "C" int hipenvs_cartpole_es_rollout_seeded(const float* state, const float* theta, int64_t p, uint32_t seed,
+                                                 double sigma, int32_t hidden, int32_t horizon, float* fitness,
+                                                 void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream) {
+  if (p < 2 || (p & 1) || p > 0x7fffffffLL || horizon < 0 || !state || !theta || !fitness || !workspace)
+    return HIPENVS_E_ARG;
+  if (hidden != 4 && hidden != 8 && hidden != 16 && hidden != 32 && hidden != 64) return HIPENVS_E_UNSUPPORTED;
+  const int64_t d = 7 * (int64_t)hidden + 2;
+  if (workspace_bytes < (int64_t)sizeof(float) * p * d) return HIPENVS_E_ARG;
+  float* population = static_cast<float*>(workspace);  // (p, d) rows, written here, read by the rollout
+  const int status = launch_perturb(theta, d, p, seed, (float)sigma, kPerturbRows, population, as_stream(stream));
+  if (status != HIPENVS_OK) return status;
+  return hipenvs_cartpole_es_rollout(state, population, p, hidden, horizon, fitness, stream);
 }

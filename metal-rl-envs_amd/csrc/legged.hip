@@ -17,7 +17,7 @@
 // (P, D) or from a column layout (D, P) in which a wave's 64 members read 256
 // contiguous bytes per weight.
 
-#include "hipenvs_device.h"
+#include "es_noise.h"
 
 namespace hipenvs {
 namespace lg {
@@ -778,6 +778,73 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_ke
 
 __global__ void set_count_kernel(uint32_t* count, uint32_t value) { *count = value; }
 
+__global__ __launch_bounds__(kBlock) void zero_pair_kernel(float* __restrict__ a, float* __restrict__ b, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  a[i] = 0.0f;
+  b[i] = 0.0f;
+}
+
+// Row of flat weight k (es.unflatten order: w1 (OBS, HID), b1, w2 (HID, OUT), b2) in the
+// unit-major tile layout.
+template <int OBS, int HID, int OUT>
+__device__ __forceinline__ int unit_row_of_flat(int k) {
+  using T = UnitRows<OBS, HID, OUT>;
+  if (k < OBS * HID) return T::w1(k / HID, k % HID);
+  k -= OBS * HID;
+  if (k < HID) return T::b1(k);
+  k -= HID;
+  if (k < HID * OUT) return T::w2(k / OUT, k % OUT);
+  return T::b2(k - HID * OUT);
+}
+
+// The first packed set of a seeded rollout: member m at slot m with its state from the
+// caller's (2N, p) rows, zero accumulators, and weights theta + sigma * (+-eps) written
+// straight into the 64-member tiles (es_noise.h generates eps). One thread per member pair
+// writes both members; the lanes of a wave are consecutive slots of one tile.
+template <int C, int HID>
+__global__ __launch_bounds__(64) void seed_set_kernel(const float* __restrict__ state,
+                                                      const float* __restrict__ theta, int64_t p, uint32_t seed,
+                                                      float sigma, Packed dst, int64_t cap) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  const int64_t half = p / 2;
+  const int64_t m = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (m >= half) return;
+  const int64_t mb = m + half;
+#pragma unroll
+  for (int r = 0; r < 2 * N; ++r) {
+    dst.state[r * cap + m] = state[r * p + m];
+    dst.state[r * cap + mb] = state[r * p + mb];
+  }
+  dst.acc[m] = 0.0f;
+  dst.acc[cap + m] = 0.0f;
+  dst.acc[mb] = 0.0f;
+  dst.acc[cap + mb] = 0.0f;
+  dst.meta[m] = (int32_t)m;
+  dst.meta[cap + m] = 0;
+  dst.meta[mb] = (int32_t)mb;
+  dst.meta[cap + mb] = 0;
+  float* wa = dst.theta + (m / kTile) * (int64_t)D * kTile + (m % kTile);
+  float* wb = dst.theta + (mb / kTile) * (int64_t)D * kTile + (mb % kTile);
+  const uint32_t key = esn::member_key(seed, (uint32_t)m);
+  for (int j = 0; j < (D + 1) / 2; ++j) {
+    float z0, z1;
+    esn::gauss_pair(key, (uint32_t)j, z0, z1);
+    const int k = 2 * j;
+    const float e0 = sigma * z0, t0 = theta[k];
+    const int u0 = unit_row_of_flat<OBS, HID, OUT>(k);
+    wa[u0 * kTile] = t0 + e0;
+    wb[u0 * kTile] = t0 + -e0;
+    if (k + 1 < D) {
+      const float e1 = sigma * z1, t1 = theta[k + 1];
+      const int u1 = unit_row_of_flat<OBS, HID, OUT>(k + 1);
+      wa[u1 * kTile] = t1 + e1;
+      wb[u1 * kTile] = t1 + -e1;
+    }
+  }
+}
+
 template <int C, int HID>
 int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32_t horizon, int iters,
                    int32_t chunk_steps, float alive, float fall, float gate, double assist, float* fitness,
@@ -834,6 +901,77 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
     cur = nxt;
   }
   return status;
+}
+
+// The seeded rollout: seed_set_kernel writes set 0 (every member, weights generated in
+// place), then every chunk runs in the compacted form, with the group tail after each.
+// Members run the same arithmetic as in launch_chunked on theta + sigma * [eps; -eps].
+template <int C, int HID>
+int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uint32_t seed, float sigma,
+                          int32_t horizon, int iters, int32_t chunk_steps, float alive, float fall, float gate,
+                          double assist, float* fitness, float* steps, void* workspace, hipStream_t s) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  const int64_t cap = round_to_tile(p);
+  char* ws = static_cast<char*>(workspace);
+  Packed set[2];
+  for (int b = 0; b < 2; ++b) {
+    set[b].state = reinterpret_cast<float*>(ws);
+    ws += sizeof(float) * 2 * N * cap;
+    set[b].theta = reinterpret_cast<float*>(ws);
+    ws += sizeof(float) * (int64_t)D * cap;
+    set[b].acc = reinterpret_cast<float*>(ws);
+    ws += sizeof(float) * 2 * cap;
+    set[b].meta = reinterpret_cast<int32_t*>(ws);
+    ws += sizeof(int32_t) * 2 * cap;
+  }
+  set[0].count = reinterpret_cast<uint32_t*>(ws);
+  set[1].count = set[0].count + 1;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rollout_chunk_kernel<C, HID, false>, 64, 0) !=
+          hipSuccess)
+    return launch_status();
+  const int64_t needed = (p + 63) / 64;
+  const int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
+  const int64_t grid = resident < needed ? resident : needed;
+  const int64_t wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * cus;
+  const int64_t tail_members = p < wide_max ? p : wide_max;
+  const int64_t tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
+  const float af = (float)assist, ad = (float)(0.1 * assist);
+  hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, (uint32_t)p);
+  hipLaunchKernelGGL((seed_set_kernel<C, HID>), dim3((unsigned)((p / 2 + 63) / 64)), dim3(64), 0, s, state, theta, p,
+                     seed, sigma, set[0], cap);
+  int status = launch_status();
+  int cur = 0;
+  for (int64_t done = 0; status == HIPENVS_OK && done < horizon; done += chunk_steps) {
+    const int nxt = 1 - cur;
+    hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[nxt].count, 0u);
+    hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state, theta, p,
+                       set[cur], set[nxt], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness,
+                       steps, wide_max);
+    hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)tail_grid), dim3(64), 0, s, set[cur], cap,
+                       horizon, iters, alive, fall, gate, af, ad, fitness, steps, wide_max);
+    status = launch_status();
+    cur = nxt;
+  }
+  return status;
+}
+
+template <int C>
+int dispatch_chunked_seeded(int32_t hidden, const float* state, const float* theta, int64_t p, uint32_t seed,
+                            float sigma, int32_t horizon, int iters, int32_t chunk_steps, float alive, float fall,
+                            float gate, double assist, float* fitness, float* steps, void* workspace,
+                            hipStream_t s) {
+  switch (hidden) {
+    case 4: return launch_chunked_seeded<C, 4>(state, theta, p, seed, sigma, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 8: return launch_chunked_seeded<C, 8>(state, theta, p, seed, sigma, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 16: return launch_chunked_seeded<C, 16>(state, theta, p, seed, sigma, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 32: return launch_chunked_seeded<C, 32>(state, theta, p, seed, sigma, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 64: return launch_chunked_seeded<C, 64>(state, theta, p, seed, sigma, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
 }
 
 template <int C>
@@ -972,6 +1110,32 @@ extern "C" int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int3
     case 1: return lg::dispatch_chunked<1>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 2: return lg::dispatch_chunked<2>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 4: return lg::dispatch_chunked<4>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+
+extern "C" int hipenvs_legged_es_rollout_seeded(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
+                                                const float* state, const float* theta, int64_t p, uint32_t seed,
+                                                double sigma, int32_t horizon, float alive_bonus,
+                                                float fall_penalty, float height_gate, double assist,
+                                                float* fitness, float* steps, void* workspace,
+                                                int64_t workspace_bytes, hipenvs_stream_t stream) {
+  if (p < 2 || (p & 1) || p > 0x7fffffffLL || horizon < 0 || iters < 0 || iters > kMaxIters || chunk_steps < 1 ||
+      !state || !theta || !fitness || !steps || !workspace)
+    return HIPENVS_E_ARG;
+  const int64_t need = hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p);
+  if (need < 0) return HIPENVS_E_UNSUPPORTED;
+  if (workspace_bytes < need) return HIPENVS_E_ARG;
+  hipStream_t s = as_stream(stream);
+  if (horizon == 0) {  // nothing to step: every member scores 0 in 0 steps
+    hipLaunchKernelGGL(lg::zero_pair_kernel, dim3(grid_for(p)), dim3(kBlock), 0, s, fitness, steps, p);
+    return launch_status();
+  }
+  const float sg = (float)sigma;
+  switch (c) {
+    case 1: return lg::dispatch_chunked_seeded<1>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 2: return lg::dispatch_chunked_seeded<2>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 4: return lg::dispatch_chunked_seeded<4>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
 }

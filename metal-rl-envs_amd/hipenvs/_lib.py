@@ -46,11 +46,18 @@ SIGNATURES = {
                                   _P, _P, _P],
     "hipenvs_legged_es_rollout_chunked": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32,
                                           ctypes.c_double, _P, _P, _P, _I64, _P],
+    "hipenvs_es_perturb": [_P, _I64, _I64, _U32, ctypes.c_double, _I32, _P, _P],
+    "hipenvs_es_update": [_P, _P, _I64, _I64, _U32, ctypes.c_double, ctypes.c_double, _P, _P, _I64, _P],
+    "hipenvs_cartpole_es_rollout_seeded": [_P, _P, _I64, _U32, ctypes.c_double, _I32, _I32, _P, _P, _I64, _P],
+    "hipenvs_acrobot_es_rollout_seeded": [_P, _P, _I64, _U32, ctypes.c_double, _I32, _I32, _P, _P, _I64, _P],
+    "hipenvs_legged_es_rollout_seeded": [_I32, _I32, _I32, _I32, _P, _P, _I64, _U32, ctypes.c_double, _I32, _F32,
+                                         _F32, _F32, ctypes.c_double, _P, _P, _P, _I64, _P],
 }
 
 # entry points that return a value rather than a status
 VALUE_SIGNATURES = {
     "hipenvs_legged_es_rollout_workspace_bytes": (ctypes.c_int64, [_I32, _I32, _I64]),
+    "hipenvs_es_update_workspace_bytes": (ctypes.c_int64, [_I64, _I64]),
 }
 
 
@@ -213,3 +220,24 @@ def check_horizon(horizon):
     if int(horizon) < 0:
         raise ValueError("horizon must be >= 0")
     return int(horizon)
+
+
+def check_population(p):
+    """An even population of at least 2 (antithetic pairs)."""
+    p = int(p)
+    if p < 2 or p % 2:
+        raise ValueError(f"the population must be even and at least 2 (antithetic pairs), got {p}")
+    return p
+
+
+def check_theta_vector(theta, d, device, name="theta"):
+    """The (d,) float32 contiguous device tensor of the unperturbed parameters."""
+    if not isinstance(theta, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(theta).__name__}")
+    if theta.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {theta.dtype}")
+    if theta.shape != (d,):
+        raise ValueError(f"{name} must have shape ({d},), got {tuple(theta.shape)}")
+    if theta.device != device:
+        raise ValueError(f"{name} is on {theta.device}, state is on {device}")
+    return theta.contiguous()

@@ -28,3 +28,22 @@ def rollout_steps(state, theta_pop, hidden, horizon):
         _lib.call("hipenvs_acrobot_es_rollout", _lib.ptr(state), _lib.ptr(theta_pop), p, hidden, horizon,
                   _lib.ptr(steps), _lib.stream_of(state.device))
     return steps
+
+
+def rollout_steps_seeded(state, theta, seed, sigma, hidden, horizon):
+    """``rollout_steps`` on the antithetic population theta + sigma * [eps; -eps] of
+    ``es_noise`` (P = state.shape[1], even), generated on the device into a (P, D)
+    workspace; asynchronous. Equals ``rollout_steps(state, es_noise.perturb(theta, P, seed,
+    sigma), hidden, horizon)`` bit for bit."""
+    p = _lib.check_population(_lib.check_state(state, 4))
+    hidden = _lib.check_hidden(hidden)
+    horizon = _lib.check_horizon(horizon)
+    d = n_params(hidden)
+    theta = _lib.check_theta_vector(theta, d, state.device)
+    workspace = torch.empty((p, d), dtype=torch.float32, device=state.device)
+    out = torch.empty(p, dtype=torch.float32, device=state.device)
+    with torch.cuda.device(state.device):
+        _lib.call("hipenvs_acrobot_es_rollout_seeded", _lib.ptr(state), _lib.ptr(theta), p, _lib.u32(seed),
+                  float(sigma), hidden, horizon, _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * 4,
+                  _lib.stream_of(state.device))
+    return out

@@ -19,8 +19,11 @@ Backends (``es.py:230-299``): ``"fused"`` runs the whole rollout as one HIP
 launch per generation (the reference's ``metal`` backend); ``"loop"`` runs the
 policy in torch and steps the HIP step kernel once per iteration (its ``mlx``
 backend). The reference's ``numpy`` backend is the CPU oracle, which this
-package does not import. Sampling, ranking and the update are torch ops on the
-GPU.
+package does not import. For these two, sampling, ranking and the update are
+torch ops on the GPU, as in the reference. ``"seeded"`` keeps the same
+generation but regenerates the antithetic noise from a counter-RNG seed inside
+the rollout and update kernels (``es_noise``), so neither the (P, D) noise nor
+the population is ever a tensor; ranking stays a torch sort.
 """
 
 import argparse
@@ -30,7 +33,7 @@ from typing import Any, Callable
 
 import torch
 
-from . import acrobot, acrobot_rollout, cartpole, cartpole_rollout, legged, legged_rollout
+from . import acrobot, acrobot_rollout, cartpole, cartpole_rollout, es_noise, legged, legged_rollout
 
 
 @dataclass(frozen=True)
@@ -44,6 +47,7 @@ class Task:
     obs: Callable              # state (D, P) -> (P, obs_dim)
     action: Callable           # logits (P, n_out) -> action index (P,) int32
     rollout: Callable          # (state, theta_pop, hidden, horizon[, assist]) -> (fitness, steps taken)
+    rollout_seeded: Callable | None = None  # (state, theta, seed, sigma, hidden, horizon[, assist]) -> same
     alive_bonus: float = 1.0
     fall_penalty: float = 0.0
     eval_bonus: float = 1.0
@@ -89,11 +93,21 @@ def steps_fitness(kernel, sign):
     return rollout
 
 
+def steps_fitness_seeded(kernel, sign):
+    """``steps_fitness`` for the seeded kernels, which take (theta, seed, sigma) for the population."""
+    def rollout(state, theta, seed, sigma, hidden, horizon):
+        steps = kernel(state, theta, seed, sigma, hidden, horizon)
+        return sign * steps, torch.clamp(steps + 1, max=horizon)
+    return rollout
+
+
 TASKS = {
     "cartpole": Task("cartpole", 4, 2, 32, 475.0, cartpole, cartpole_obs, argmax_action,
-                     steps_fitness(cartpole_rollout.rollout_steps, 1.0)),
+                     steps_fitness(cartpole_rollout.rollout_steps, 1.0),
+                     steps_fitness_seeded(cartpole_rollout.rollout_steps_seeded, 1.0)),
     "acrobot": Task("acrobot", 6, 3, 32, -100.0, acrobot, acrobot_obs, argmax_action,
-                    steps_fitness(acrobot_rollout.rollout_steps, -1.0)),
+                    steps_fitness(acrobot_rollout.rollout_steps, -1.0),
+                    steps_fitness_seeded(acrobot_rollout.rollout_steps_seeded, -1.0)),
 }
 
 
@@ -105,8 +119,12 @@ def legged_task(c, name, alive=1.0, fall=0.0, gate=0.0, hidden=16, iters=legged.
     def rollout(state, theta_pop, hidden_, horizon, assist=0.0):
         return legged_rollout.rollout(state, theta_pop, hidden_, horizon, c, alive, fall, gate, assist, iters)
 
+    def rollout_seeded(state, theta, seed, sigma, hidden_, horizon, assist=0.0):
+        return legged_rollout.rollout_seeded(state, theta, seed, sigma, hidden_, horizon, c, alive, fall, gate,
+                                             assist, iters)
+
     return Task(f"legged{c}{name}", 5 + 2 * c, 3 * c, hidden, 100.0, env, legged_obs, legged_action(c), rollout,
-                alive, fall, 0.0, gate, 3 + c, True)
+                rollout_seeded, alive, fall, 0.0, gate, 3 + c, True)
 
 
 for _c, _name, _kw in ((2, "", {}), (4, "", {}), (2, "_distance", {"alive": 0.0}), (4, "_distance", {"alive": 0.0}),
@@ -225,7 +243,39 @@ class LoopBackend(FusedBackend):
         return loop_fitness(self, unflatten(theta_pop, hidden, self.task), horizon, assist, start_velocity)
 
 
-BACKENDS = {"fused": FusedBackend, "loop": LoopBackend}
+class SeededBackend(FusedBackend):
+    """Fused rollouts on a population regenerated from a counter-RNG seed (``es_noise``): one
+    seed per generation drives both the rollout's population and the update's noise."""
+
+    name = "seeded"
+
+    def __init__(self, task, seed, device=None):
+        if task.rollout_seeded is None:
+            raise ValueError(f"task {task.name} has no seeded rollout")
+        super().__init__(task, seed, device)
+        self.noise_counter = (seed * 0x9E3779B9) & 0xFFFFFFFF
+
+    def next_noise_seed(self):
+        self.noise_counter = (self.noise_counter + 1) & 0xFFFFFFFF
+        return self.noise_counter
+
+    def rollout_seeded(self, theta, seed, sigma, pop, hidden, horizon, assist=0.0, start_velocity=0.0):
+        state = push(self.task, self.reset(pop), start_velocity)
+        if self.task.assistable:
+            return self.task.rollout_seeded(state, theta, seed, sigma, hidden, horizon, assist)
+        return self.task.rollout_seeded(state, theta, seed, sigma, hidden, horizon)
+
+    def generation(self, theta, cfg, hidden, gen=1):
+        """``es.py:218-227`` with the noise of one seed: rollout, centered ranks, update."""
+        seed = self.next_noise_seed()
+        assist, start_velocity = curriculum(cfg, gen)
+        fit, steps = self.rollout_seeded(theta, seed, cfg.sigma, cfg.pop, hidden, cfg.horizon, assist,
+                                         start_velocity)
+        theta = es_noise.update(theta, centered_ranks(fit), seed, cfg.sigma, cfg.lr)
+        return theta, fit, steps
+
+
+BACKENDS = {"fused": FusedBackend, "loop": LoopBackend, "seeded": SeededBackend}
 
 
 def loop_fitness(backend, params, horizon, assist=0.0, start_velocity=0.0, state=None):
@@ -254,6 +304,8 @@ def loop_fitness(backend, params, horizon, assist=0.0, start_velocity=0.0, state
 
 def generation(backend, theta, cfg, hidden, gen=1):
     """One ES generation (``es.py:218-227``): antithetic noise, rollout, ranks, update."""
+    if isinstance(backend, SeededBackend):
+        return backend.generation(theta, cfg, hidden, gen)
     half = backend.normal((cfg.pop // 2, theta.shape[0]))
     eps = torch.cat([half, -half], dim=0)
     assist, start_velocity = curriculum(cfg, gen)

@@ -80,3 +80,33 @@ def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=
             _lib.call("hipenvs_legged_es_rollout", c, hidden, int(iters), LAYOUTS[schedule], _lib.ptr(state),
                       _lib.ptr(theta_pop), p, horizon, *args, _lib.stream_of(state.device))
     return fitness, steps
+
+
+def rollout_seeded(state, theta, seed, sigma, hidden, horizon, c, alive_bonus=1.0, fall_penalty=0.0,
+                   height_gate=0.0, assist=0.0, iters=8, chunk_steps=CHUNK_STEPS):
+    """The chunked rollout on the antithetic population theta + sigma * [eps; -eps] of
+    ``es_noise`` (P = state.shape[1], even). The weights are generated on the device straight
+    into the packed member tiles of the workspace, so no (P, D) tensor is made. Equals
+    ``rollout(state, es_noise.perturb(theta, P, seed, sigma), hidden, horizon, c, ...)`` bit
+    for bit. Returns (fitness (P,), steps (P,)); asynchronous."""
+    if int(c) not in SUPPORTED_C:
+        raise ValueError(f"c must be one of {SUPPORTED_C}, got {c}")
+    if not 0 <= int(iters) <= 4096:
+        raise ValueError("iters must be in [0, 4096]")
+    if int(chunk_steps) < 1:
+        raise ValueError("chunk_steps must be >= 1")
+    c = int(c)
+    p = _lib.check_population(_lib.check_state(state, 2 * (3 + c)))
+    hidden = _lib.check_hidden(hidden)
+    horizon = _lib.check_horizon(horizon)
+    theta = _lib.check_theta_vector(theta, n_params(hidden, c), state.device)
+    fitness = torch.empty(p, dtype=torch.float32, device=state.device)
+    steps = torch.empty(p, dtype=torch.float32, device=state.device)
+    nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=state.device)
+    with torch.cuda.device(state.device):
+        _lib.call("hipenvs_legged_es_rollout_seeded", c, hidden, int(iters), int(chunk_steps), _lib.ptr(state),
+                  _lib.ptr(theta), p, _lib.u32(seed), float(sigma), horizon, float(alive_bonus),
+                  float(fall_penalty), float(height_gate), float(assist), _lib.ptr(fitness), _lib.ptr(steps),
+                  _lib.ptr(workspace), nbytes, _lib.stream_of(state.device))
+    return fitness, steps
