@@ -34,7 +34,15 @@ sample of about `--cpu-seconds` seconds on this host.
 * `cartpole_fused_k32`: the K = 32 fused CartPole step, in-kernel and array actions;
 * `es_config2`: CartPole and Acrobot fused ES rollouts, P = 4,096, H = 32, horizon 500;
 * `aba_euler`: the K-link pendulum, semi-implicit Euler dt 0.01, N = 65,536,
-  K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B).
+  K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B);
+* `es_generation`: one whole ES generation (noise, rollout, centered ranks,
+  update) two ways: "materialised" is the reference's generation (es.py:218-227)
+  in torch around the fused rollout ((P/2, D) randn, concatenated noise,
+  population, rank-weighted sum); "seeded" regenerates the noise from a
+  counter-RNG seed inside the rollout and update kernels. Wall time (median of
+  repeats) and peak allocated device memory, for CartPole and Acrobot at
+  P = 4,096, H = 32, horizon 500 and legged4 at N = 262,144, H = 64, S = 8,
+  horizon 1,000.
 
 Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--sweep] [--skip-cpu] [--only cartpole|legged]
 """
@@ -442,6 +450,65 @@ def cpu_baseline_legged(n, seconds, c=4, hidden=64, sweeps=8):
 # ES config 2 and ABA config 3
 # ---------------------------------------------------------------------------
 
+def bench_es_generation(dev, repeats, legged_n, legged_horizon):
+    import torch
+
+    from hipenvs import (acrobot, acrobot_rollout, cartpole, cartpole_rollout, es, es_noise, legged,
+                         legged_rollout)
+
+    cases = (
+        ("cartpole", 4096, 32, 500, 0.1, cartpole.reset,
+         lambda st, pop: cartpole_rollout.rollout_steps(st, pop, 32, 500),
+         lambda st, th, sd: cartpole_rollout.rollout_steps_seeded(st, th, sd, 0.1, 32, 500)),
+        ("acrobot", 4096, 32, 500, 0.1, acrobot.reset,
+         lambda st, pop: acrobot_rollout.rollout_steps(st, pop, 32, 500),
+         lambda st, th, sd: acrobot_rollout.rollout_steps_seeded(st, th, sd, 0.1, 32, 500)),
+        ("legged4", legged_n, 64, legged_horizon, 0.03, legged.Legged(4).reset,
+         lambda st, pop: legged_rollout.rollout(st, pop, 64, legged_horizon, 4)[0],
+         lambda st, th, sd: legged_rollout.rollout_seeded(st, th, sd, 0.03, 64, legged_horizon, 4)[0]),
+    )
+    out = {}
+    for name, p, hidden, horizon, sigma, reset, roll, roll_seeded in cases:
+        d = {"cartpole": 7 * hidden + 2, "acrobot": 10 * hidden + 3}.get(name) or legged_rollout.n_params(hidden, 4)
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        theta = torch.randn(d, generator=g, device=dev) * 0.1
+        state = reset(p, seed=0, device=dev)
+        lr = 0.1
+
+        def materialised():
+            half = torch.randn((p // 2, d), generator=g, device=dev)
+            eps = torch.cat([half, -half])
+            fit = roll(state, theta[None, :] + sigma * eps)
+            grad = (es.centered_ranks(fit)[:, None] * eps).sum(dim=0) / (p * sigma)
+            return theta + lr * grad
+
+        def seeded():
+            fit = roll_seeded(state, theta, 7)
+            return es_noise.update(theta, es.centered_ranks(fit), 7, sigma, lr)
+
+        rec = {"P": p, "D": d, "hidden": hidden, "horizon": horizon}
+        for label, fn in (("materialised", materialised), ("seeded", seeded)):
+            fn()
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats(dev)
+            walls = []
+            for _ in range(repeats):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                walls.append(time.perf_counter() - t0)
+            rec[label] = {"generation_ms": statistics.median(walls) * 1e3,
+                          "peak_alloc_gib": torch.cuda.max_memory_allocated(dev) / 2**30}
+        log(f"ES generation {name} P={p} D={d}: materialised {rec['materialised']['generation_ms']:.2f} ms "
+            f"({rec['materialised']['peak_alloc_gib']:.2f} GiB), seeded {rec['seeded']['generation_ms']:.2f} ms "
+            f"({rec['seeded']['peak_alloc_gib']:.2f} GiB)")
+        out[name] = rec
+        del state, theta
+    return out
+
+
 def bench_es_config2(dev, repeats):
     import torch
 
@@ -553,6 +620,7 @@ def main():
         extra["legged4_es_rollout"] = legged
     if args.only is None:
         extra["es_config2"] = bench_es_config2(dev, args.repeats)
+        extra["es_generation"] = bench_es_generation(dev, args.repeats, args.legged_n, args.legged_horizon)
         extra["aba_euler"] = bench_aba(dev)
 
     cpu = None
