@@ -42,7 +42,11 @@ sample of about `--cpu-seconds` seconds on this host.
   counter-RNG seed inside the rollout and update kernels. Wall time (median of
   repeats) and peak allocated device memory, for CartPole and Acrobot at
   P = 4,096, H = 32, horizon 500 and legged4 at N = 262,144, H = 64, S = 8,
-  horizon 1,000.
+  horizon 1,000;
+* `es_evaluate`: the learner's greedy evaluation of the mean policy (es.py:308-322,
+  2,048 envs x 500 steps): the fused one-launch kernel against the reference's
+  loop (torch mean policy + one env-step launch per iteration); wall time, median
+  of repeats, and both scores.
 
 Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--sweep] [--skip-cpu] [--only cartpole|legged]
 """
@@ -509,6 +513,35 @@ def bench_es_generation(dev, repeats, legged_n, legged_horizon):
     return out
 
 
+def bench_es_evaluate(dev, repeats):
+    import torch
+
+    from hipenvs import es
+
+    out = {}
+    for name, hidden in (("cartpole", 32), ("acrobot", 32), ("legged4", 64)):
+        task = es.TASKS[name]
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        theta = torch.randn(es.n_params(hidden, task), generator=g, device=dev) * 0.1
+        rec = {"n": 2048, "steps": 500, "hidden": hidden}
+        for label, fn in (("fused", lambda: es.evaluate_theta(task, theta, hidden, device=dev)),
+                          ("loop", lambda: es.evaluate(task, es.mean_policy(theta, hidden, task), device=dev))):
+            score = fn()
+            walls = []
+            for _ in range(repeats):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                walls.append(time.perf_counter() - t0)
+            rec[label] = {"ms": statistics.median(walls) * 1e3, "score": score}
+        log(f"ES evaluate {name}: fused {rec['fused']['ms']:.2f} ms (score {rec['fused']['score']:.3f}), "
+            f"loop {rec['loop']['ms']:.2f} ms (score {rec['loop']['score']:.3f})")
+        out[name] = rec
+    return out
+
+
 def bench_es_config2(dev, repeats):
     import torch
 
@@ -621,6 +654,7 @@ def main():
     if args.only is None:
         extra["es_config2"] = bench_es_config2(dev, args.repeats)
         extra["es_generation"] = bench_es_generation(dev, args.repeats, args.legged_n, args.legged_horizon)
+        extra["es_evaluate"] = bench_es_evaluate(dev, args.repeats)
         extra["aba_euler"] = bench_aba(dev)
 
     cpu = None

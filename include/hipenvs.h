@@ -208,6 +208,31 @@ int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, 
                                       float* fitness, float* steps, void* workspace, int64_t workspace_bytes,
                                       hipenvs_stream_t stream);
 
+/* ---- Greedy evaluation of one policy ----------------------------------- */
+/* The reference's evaluate (es.py:308-322) steps n fresh envs with the mean
+ * policy for `steps` steps through the env step and sums, per env,
+ * (reward - 1 + eval_bonus) while no termination has happened. These run the
+ * whole loop in one launch with theta (D) shared by every env (es.unflatten's
+ * layout), stopping each env at its first termination, which adds nothing,
+ * and write the per-env sum to fitness (n) f32; its mean is the score.
+ * hidden in {4, 8, 16, 32, 64}; the policy sums as the fused rollouts do. */
+
+/* CartPole: reward 1, eval_bonus 1 -> steps survived.
+ * Replaces evaluate with mean_policy for the CartPole task (es.py:302-322). */
+int hipenvs_cartpole_evaluate(const float* state, const float* theta, int64_t n, int32_t hidden, int32_t steps,
+                              float* fitness, hipenvs_stream_t stream);
+
+/* Acrobot: reward -1, eval_bonus 1 -> minus the steps before the tip clears height 1.
+ * Replaces evaluate for the Acrobot task (es.py:302-322). */
+int hipenvs_acrobot_evaluate(const float* state, const float* theta, int64_t n, int32_t hidden, int32_t steps,
+                             float* fitness, hipenvs_stream_t stream);
+
+/* Legged body with c in {1, 2, 4}, no assist: sum of ((v_x + 1) - 1) + eval_bonus
+ * while standing (the reference's legged tasks use eval_bonus 0: forward distance).
+ * Replaces evaluate for the legged tasks (es.py:302-322, legged_np.py:114-121). */
+int hipenvs_legged_evaluate(int32_t c, int32_t hidden, int32_t iters, const float* state, const float* theta,
+                            int64_t n, int32_t steps, float eval_bonus, float* fitness, hipenvs_stream_t stream);
+
 /* ---- Seeded ES generation ---------------------------------------------- */
 /* The reference's generation (es.py:218-227) draws half = (P/2, D) normals,
  * materialises eps = [half; -half] and theta + sigma * eps, and reduces

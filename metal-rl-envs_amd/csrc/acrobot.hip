@@ -119,11 +119,12 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
 // at the first termination. acrobot_rollout_metal.py:21-58.
 template <int H>
 __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
-                                                     int64_t p, int32_t horizon, float* __restrict__ steps_out) {
+                                                     int64_t member_stride, int64_t p, int32_t horizon,
+                                                     float out_sign, float* __restrict__ steps_out) {
   constexpr int D = 10 * H + 3;
   const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (i >= p) return;
-  const float* row = theta + i * D;
+  const float* row = theta + i * member_stride;
   float w[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) w[d] = row[d];
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
     if (terminal(s)) break;
     steps += 1.0f;
   }
-  steps_out[i] = steps;
+  steps_out[i] = out_sign * steps + 0.0f;  // + 0: a score of -0 reads +0
 }
 
 // The same rollout with a group of kRolloutLanes lanes per member (four members to a
@@ -167,8 +168,9 @@ constexpr int kRolloutMembers = 64 / kRolloutLanes;
 
 template <int H>
 __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restrict__ state,
-                                                           const float* __restrict__ theta, int64_t p,
-                                                           int32_t horizon, float* __restrict__ steps_out) {
+                                                           const float* __restrict__ theta, int64_t member_stride,
+                                                           int64_t p, int32_t horizon, float out_sign,
+                                                           float* __restrict__ steps_out) {
   constexpr int D = 10 * H + 3, G = kRolloutLanes, U = (H + G - 1) / G;
   __shared__ float xh_all[kRolloutMembers * H];
   __shared__ float xl_all[kRolloutMembers * 4];
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
   const int64_t i = (int64_t)blockIdx.x * kRolloutMembers + mloc;
   bool alive = i < p;
   const int64_t m = alive ? i : p - 1;  // a group past p steps member p - 1, unused
-  const float* row = theta + m * D;
+  const float* row = theta + m * member_stride;
   float w1[U][6], b1[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -234,18 +236,27 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
       }
     }
   }
-  if (g == 0 && i < p) steps_out[i] = steps;
+  if (g == 0 && i < p) steps_out[i] = out_sign * steps + 0.0f;  // + 0: a score of -0 reads +0
+}
+
+// member_stride D and out_sign 1 for a population's rollout; stride 0 (one shared policy)
+// and sign -1 for the greedy evaluation, whose per-env score is minus the steps.
+template <int H>
+int launch_rollout(const float* state, const float* theta, int64_t member_stride, int64_t p, int32_t horizon,
+                   float out_sign, float* out, hipStream_t s) {
+  if (p <= group_rollout_limit()) {
+    hipLaunchKernelGGL(rollout_group_kernel<H>, dim3((unsigned)((p + kRolloutMembers - 1) / kRolloutMembers)),
+                       dim3(64), 0, s, state, theta, member_stride, p, horizon, out_sign, out);
+  } else {
+    hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, member_stride, p,
+                       horizon, out_sign, out);
+  }
+  return launch_status();
 }
 
 template <int H>
 int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
-  if (p <= group_rollout_limit()) {
-    hipLaunchKernelGGL(rollout_group_kernel<H>, dim3((unsigned)((p + kRolloutMembers - 1) / kRolloutMembers)),
-                       dim3(64), 0, s, state, theta, p, horizon, out);
-  } else {
-    hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
-  }
-  return launch_status();
+  return launch_rollout<H>(state, theta, (int64_t)(10 * H + 3), p, horizon, 1.0f, out, s);
 }
 
 }  // namespace ac
@@ -296,4 +307,19 @@ extern "C" int hipenvs_acrobot_es_rollout_seeded(const float* state, const float
   const int status = launch_perturb(theta, d, p, seed, (float)sigma, kPerturbRows, population, as_stream(stream));
   if (status != HIPENVS_OK) return status;
   return hipenvs_acrobot_es_rollout(state, population, p, hidden, horizon, steps, stream);
+}
+
+extern "C" int hipenvs_acrobot_evaluate(const float* state, const float* theta, int64_t n, int32_t hidden,
+                                        int32_t steps, float* fitness, hipenvs_stream_t stream) {
+  if (n < 0 || steps < 0 || (n > 0 && (!state || !theta || !fitness))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  switch (hidden) {  // every env reads the one policy: member stride 0; score = -steps
+    case 4: return ac::launch_rollout<4>(state, theta, 0, n, steps, -1.0f, fitness, s);
+    case 8: return ac::launch_rollout<8>(state, theta, 0, n, steps, -1.0f, fitness, s);
+    case 16: return ac::launch_rollout<16>(state, theta, 0, n, steps, -1.0f, fitness, s);
+    case 32: return ac::launch_rollout<32>(state, theta, 0, n, steps, -1.0f, fitness, s);
+    case 64: return ac::launch_rollout<64>(state, theta, 0, n, steps, -1.0f, fitness, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
 }

@@ -135,14 +135,17 @@ __global__ __launch_bounds__(kBlock) void sample_actions_kernel(int32_t* __restr
 // registers (es.unflatten layout: w1 (4, H), b1 (H), w2 (H, 2), b2 (2)), the
 // 4-H-2 tanh policy with first-index argmax, the step physics, and an early
 // exit at the first termination; writes the steps survived (the terminating
-// step not counted). cartpole_rollout_metal.py:46-77.
+// step not counted). cartpole_rollout_metal.py:46-77. Member i's weights start
+// at theta + i * member_stride: D for a population, 0 for one policy shared by
+// every env (the greedy evaluation).
 template <int H>
 __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ state, const float* __restrict__ theta,
-                                                     int64_t p, int32_t horizon, float* __restrict__ fitness) {
-  constexpr int D = 7 * H + 2;
+                                                     int64_t member_stride, int64_t p, int32_t horizon,
+                                                     float* __restrict__ fitness) {
   const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (i >= p) return;
-  const float* row = theta + i * D;
+  constexpr int D = 7 * H + 2;
+  const float* row = theta + i * member_stride;
   float w[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) w[d] = row[d];
@@ -174,8 +177,8 @@ constexpr int kRolloutMembers = 64 / kRolloutLanes;
 
 template <int H>
 __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restrict__ state,
-                                                           const float* __restrict__ theta, int64_t p,
-                                                           int32_t horizon, float* __restrict__ fitness) {
+                                                           const float* __restrict__ theta, int64_t member_stride,
+                                                           int64_t p, int32_t horizon, float* __restrict__ fitness) {
   constexpr int D = 7 * H + 2, G = kRolloutLanes, U = (H + G - 1) / G;
   __shared__ float xh_all[kRolloutMembers * H];
   __shared__ float xl_all[kRolloutMembers * 2];
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
   const int64_t i = (int64_t)blockIdx.x * kRolloutMembers + mloc;
   bool alive = i < p;
   const int64_t m = alive ? i : p - 1;  // a group past p steps member p - 1, unused
-  const float* row = theta + m * D;
+  const float* row = theta + m * member_stride;
   float w1[U][4], b1[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -234,14 +237,21 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
 }
 
 template <int H>
-int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
+int launch_rollout(const float* state, const float* theta, int64_t member_stride, int64_t p, int32_t horizon,
+                   float* out, hipStream_t s) {
   if (p <= group_rollout_limit()) {
     hipLaunchKernelGGL(rollout_group_kernel<H>, dim3((unsigned)((p + kRolloutMembers - 1) / kRolloutMembers)),
-                       dim3(64), 0, s, state, theta, p, horizon, out);
+                       dim3(64), 0, s, state, theta, member_stride, p, horizon, out);
   } else {
-    hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, p, horizon, out);
+    hipLaunchKernelGGL(rollout_kernel<H>, dim3(grid_for(p, 64)), dim3(64), 0, s, state, theta, member_stride, p,
+                       horizon, out);
   }
   return launch_status();
+}
+
+template <int H>
+int launch_rollout(const float* state, const float* theta, int64_t p, int32_t horizon, float* out, hipStream_t s) {
+  return launch_rollout<H>(state, theta, (int64_t)(7 * H + 2), p, horizon, out, s);
 }
 
 }  // namespace cp
@@ -316,4 +326,19 @@ extern "C" int hipenvs_cartpole_es_rollout_seeded(const float* state, const floa
   const int status = launch_perturb(theta, d, p, seed, (float)sigma, kPerturbRows, population, as_stream(stream));
   if (status != HIPENVS_OK) return status;
   return hipenvs_cartpole_es_rollout(state, population, p, hidden, horizon, fitness, stream);
+}
+
+extern "C" int hipenvs_cartpole_evaluate(const float* state, const float* theta, int64_t n, int32_t hidden,
+                                         int32_t steps, float* fitness, hipenvs_stream_t stream) {
+  if (n < 0 || steps < 0 || (n > 0 && (!state || !theta || !fitness))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  switch (hidden) {  // every env reads the one policy: member stride 0
+    case 4: return cp::launch_rollout<4>(state, theta, 0, n, steps, fitness, s);
+    case 8: return cp::launch_rollout<8>(state, theta, 0, n, steps, fitness, s);
+    case 16: return cp::launch_rollout<16>(state, theta, 0, n, steps, fitness, s);
+    case 32: return cp::launch_rollout<32>(state, theta, 0, n, steps, fitness, s);
+    case 64: return cp::launch_rollout<64>(state, theta, 0, n, steps, fitness, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
 }

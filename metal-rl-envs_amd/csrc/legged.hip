@@ -560,6 +560,37 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_kernel(c
   steps_out[e] = taken;
 }
 
+// The greedy evaluation of one policy (es.py:308-322): every env runs the shared weights
+// theta (D) without assist from its own start state for up to `steps` steps. While the body
+// stands, the score adds the evaluation's term (reward - 1) + eval_bonus with the
+// environment's reward v_x + 1 (legged_np.py:118-121); the step that falls adds nothing
+// and ends the episode. All lanes read the same weight at once.
+template <int C, int HID>
+__global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void evaluate_kernel(const float* __restrict__ state,
+                                                                             const float* __restrict__ theta,
+                                                                             int64_t n, int32_t steps, int iters,
+                                                                             float eval_bonus,
+                                                                             float* __restrict__ fitness) {
+  constexpr int N = 3 + C;
+  const int64_t e = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (e >= n) return;
+  float q[N], v[N], tq[C];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = state[i * n + e];
+    v[i] = state[(N + i) * n + e];
+  }
+  float total = 0.0f;
+  for (int32_t t = 0; t < steps; ++t) {
+    policy_torques<C, HID>(theta, 1, q, v, tq);
+#pragma unroll 1
+    for (int s = 0; s < SUBSTEPS; ++s) substep_exact<C>(q, v, tq, iters, 0.0f, 0.0f);
+    if (fallen<C>(q)) break;
+    total = total + (((v[0] + 1.0f) - 1.0f) + eval_bonus);
+  }
+  fitness[e] = total;
+}
+
 // Compacting schedule for the fused rollout. Episode lengths are heavy-tailed
 // (at the ES benchmark's shape the mean is ~43 steps while a few members last
 // the whole horizon), and a one-member-per-lane launch keeps each wave busy
@@ -975,6 +1006,21 @@ int dispatch_chunked_seeded(int32_t hidden, const float* state, const float* the
 }
 
 template <int C>
+int launch_evaluate(int32_t hidden, const float* state, const float* theta, int64_t n, int32_t steps, int iters,
+                    float eval_bonus, float* fitness, hipStream_t s) {
+  const dim3 grid(grid_for(n, 64)), block(64);
+  switch (hidden) {
+    case 4: hipLaunchKernelGGL((evaluate_kernel<C, 4>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+    case 8: hipLaunchKernelGGL((evaluate_kernel<C, 8>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+    case 16: hipLaunchKernelGGL((evaluate_kernel<C, 16>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+    case 32: hipLaunchKernelGGL((evaluate_kernel<C, 32>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+    case 64: hipLaunchKernelGGL((evaluate_kernel<C, 64>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+template <int C>
 int dispatch_chunked(int32_t hidden, const float* state, const float* theta_cols, int64_t p, int32_t horizon,
                      int iters, int32_t chunk_steps, float alive, float fall, float gate, double assist,
                      float* fitness, float* steps, void* workspace, hipStream_t s) {
@@ -1136,6 +1182,21 @@ extern "C" int hipenvs_legged_es_rollout_seeded(int32_t c, int32_t hidden, int32
     case 1: return lg::dispatch_chunked_seeded<1>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 2: return lg::dispatch_chunked_seeded<2>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 4: return lg::dispatch_chunked_seeded<4>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+
+extern "C" int hipenvs_legged_evaluate(int32_t c, int32_t hidden, int32_t iters, const float* state,
+                                       const float* theta, int64_t n, int32_t steps, float eval_bonus,
+                                       float* fitness, hipenvs_stream_t stream) {
+  if (n < 0 || steps < 0 || iters < 0 || iters > kMaxIters || (n > 0 && (!state || !theta || !fitness)))
+    return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipStream_t s = as_stream(stream);
+  switch (c) {
+    case 1: return lg::launch_evaluate<1>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
+    case 2: return lg::launch_evaluate<2>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
+    case 4: return lg::launch_evaluate<4>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
 }

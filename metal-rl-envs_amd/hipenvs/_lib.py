@@ -46,6 +46,9 @@ SIGNATURES = {
                                   _P, _P, _P],
     "hipenvs_legged_es_rollout_chunked": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32,
                                           ctypes.c_double, _P, _P, _P, _I64, _P],
+    "hipenvs_cartpole_evaluate": [_P, _P, _I64, _I32, _I32, _P, _P],
+    "hipenvs_acrobot_evaluate": [_P, _P, _I64, _I32, _I32, _P, _P],
+    "hipenvs_legged_evaluate": [_I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _P, _P],
     "hipenvs_es_perturb": [_P, _I64, _I64, _U32, ctypes.c_double, _I32, _P, _P],
     "hipenvs_es_update": [_P, _P, _I64, _I64, _U32, ctypes.c_double, ctypes.c_double, _P, _P, _I64, _P],
     "hipenvs_cartpole_es_rollout_seeded": [_P, _P, _I64, _U32, ctypes.c_double, _I32, _I32, _P, _P, _I64, _P],

@@ -46,3 +46,19 @@ def rollout_steps_seeded(state, theta, seed, sigma, hidden, horizon):
                   float(sigma), hidden, horizon, _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * 4,
                   _lib.stream_of(state.device))
     return out
+
+
+def evaluate(state, theta, hidden, steps):
+    """Per-env score of the greedy policy ``theta`` (D,) shared by every env of `state` (4, n)
+    over up to ``steps`` steps: the reference's evaluation sum (``es.py:308-322``) of
+    reward - 1 + 1 to the first termination, i.e. steps survived. One launch; asynchronous.
+    Returns (n,) float32; ``.mean()`` is the canonical score."""
+    n = _lib.check_state(state, 4)
+    hidden = _lib.check_hidden(hidden)
+    steps = _lib.check_horizon(steps)
+    theta = _lib.check_theta_vector(theta, n_params(hidden), state.device)
+    out = torch.empty(n, dtype=torch.float32, device=state.device)
+    with torch.cuda.device(state.device):
+        _lib.call("hipenvs_cartpole_evaluate", _lib.ptr(state), _lib.ptr(theta), n, hidden, steps, _lib.ptr(out),
+                  _lib.stream_of(state.device))
+    return out

@@ -54,6 +54,7 @@ class Task:
     height_gate: float = 0.0
     xdot_row: int | None = None
     assistable: bool = False
+    evaluate_policy: Callable | None = None  # (state, theta, hidden, steps) -> per-env score, one launch
 
 
 def argmax_action(logits):
@@ -104,10 +105,12 @@ def steps_fitness_seeded(kernel, sign):
 TASKS = {
     "cartpole": Task("cartpole", 4, 2, 32, 475.0, cartpole, cartpole_obs, argmax_action,
                      steps_fitness(cartpole_rollout.rollout_steps, 1.0),
-                     steps_fitness_seeded(cartpole_rollout.rollout_steps_seeded, 1.0)),
+                     steps_fitness_seeded(cartpole_rollout.rollout_steps_seeded, 1.0),
+                     evaluate_policy=cartpole_rollout.evaluate),
     "acrobot": Task("acrobot", 6, 3, 32, -100.0, acrobot, acrobot_obs, argmax_action,
                     steps_fitness(acrobot_rollout.rollout_steps, -1.0),
-                    steps_fitness_seeded(acrobot_rollout.rollout_steps_seeded, -1.0)),
+                    steps_fitness_seeded(acrobot_rollout.rollout_steps_seeded, -1.0),
+                    evaluate_policy=acrobot_rollout.evaluate),
 }
 
 
@@ -123,8 +126,11 @@ def legged_task(c, name, alive=1.0, fall=0.0, gate=0.0, hidden=16, iters=legged.
         return legged_rollout.rollout_seeded(state, theta, seed, sigma, hidden_, horizon, c, alive, fall, gate,
                                              assist, iters)
 
+    def evaluate_policy(state, theta, hidden_, steps):
+        return legged_rollout.evaluate(state, theta, hidden_, steps, c, iters, eval_bonus=0.0)
+
     return Task(f"legged{c}{name}", 5 + 2 * c, 3 * c, hidden, 100.0, env, legged_obs, legged_action(c), rollout,
-                rollout_seeded, alive, fall, 0.0, gate, 3 + c, True)
+                rollout_seeded, alive, fall, 0.0, gate, 3 + c, True, evaluate_policy)
 
 
 for _c, _name, _kw in ((2, "", {}), (4, "", {}), (2, "_distance", {"alive": 0.0}), (4, "_distance", {"alive": 0.0}),
@@ -335,6 +341,17 @@ def evaluate(task, actor, n=2048, steps=500, device=None, seed=0x7FFF0000):
     return fit.mean().item()
 
 
+def evaluate_theta(task, theta, hidden, n=2048, steps=500, device=None, seed=0x7FFF0000):
+    """``evaluate(task, mean_policy(theta, hidden, task), n, steps)`` (``es.py:302-322``) as one
+    launch of the task's fused evaluation kernel when it has one; the per-env sums are the
+    reference's, with the policy summed in the fused rollouts' order instead of a matmul's."""
+    if task.evaluate_policy is None:
+        return evaluate(task, mean_policy(theta, hidden, task), n, steps, device, seed)
+    device = torch.device(device) if device is not None else theta.device
+    state = task.env.reset(n, seed=seed, device=device)
+    return task.evaluate_policy(state, theta, hidden, steps).mean().item()
+
+
 @dataclass
 class Result:
     solved: bool
@@ -361,7 +378,7 @@ def train(cfg, backend_name, seed, log=lambda *_: None, device=None):
         torch.cuda.synchronize(backend.device)
         train_seconds += time.perf_counter() - start
         env_steps += int(steps.sum().item())
-        score = evaluate(task, mean_policy(theta, hidden, task), device=backend.device)
+        score = evaluate_theta(task, theta, hidden, device=backend.device)
         log(gen, env_steps, train_seconds, float(fit.mean().item()), score)
         if score >= solved_at:
             return Result(True, gen, env_steps, train_seconds, score)

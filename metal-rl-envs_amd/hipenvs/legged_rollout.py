@@ -110,3 +110,24 @@ def rollout_seeded(state, theta, seed, sigma, hidden, horizon, c, alive_bonus=1.
                   float(fall_penalty), float(height_gate), float(assist), _lib.ptr(fitness), _lib.ptr(steps),
                   _lib.ptr(workspace), nbytes, _lib.stream_of(state.device))
     return fitness, steps
+
+
+def evaluate(state, theta, hidden, steps, c, iters=8, eval_bonus=0.0):
+    """Per-env score of the greedy policy ``theta`` (D,) shared by every env of `state`
+    (2(3+C), n), without assist, over up to ``steps`` steps: the reference's evaluation sum
+    (``es.py:308-322``) of (reward - 1) + eval_bonus with reward v_x + 1 while the body stands
+    (forward distance for eval_bonus 0), ending at the first fall. One launch; asynchronous."""
+    if int(c) not in SUPPORTED_C:
+        raise ValueError(f"c must be one of {SUPPORTED_C}, got {c}")
+    if not 0 <= int(iters) <= 4096:
+        raise ValueError("iters must be in [0, 4096]")
+    c = int(c)
+    n = _lib.check_state(state, 2 * (3 + c))
+    hidden = _lib.check_hidden(hidden)
+    steps = _lib.check_horizon(steps)
+    theta = _lib.check_theta_vector(theta, n_params(hidden, c), state.device)
+    out = torch.empty(n, dtype=torch.float32, device=state.device)
+    with torch.cuda.device(state.device):
+        _lib.call("hipenvs_legged_evaluate", c, hidden, int(iters), _lib.ptr(state), _lib.ptr(theta), n, steps,
+                  float(eval_bonus), _lib.ptr(out), _lib.stream_of(state.device))
+    return out

@@ -12,6 +12,9 @@ TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
 * ``loop_fitness``: ``es.py:174-193``: step the whole population once per
   iteration with auto-reset, count ``steps += alive``, then
   ``fit += (forward + alive_bonus) * alive - fall_penalty * fell``.
+* ``evaluate_loop``: ``es.py:308-322``: every env steps each iteration with
+  auto-reset, ``alive &= ~done``, ``fit += (reward - 1 + eval_bonus) * alive``
+  in float32 (MLX's default dtype for ``mx.zeros``).
 """
 
 import numpy as np
@@ -102,3 +105,18 @@ def generation_update(theta, eps, fitness, sigma, lr):
     ranks = centered_ranks(np.asarray(fitness, dtype=F32))
     grad = (ranks[:, None] * eps).sum(axis=0) / (p * sigma)
     return theta + lr * grad
+
+
+def evaluate_loop(step, action_of, state, steps, seed0, eval_bonus=1.0):
+    """Per-env sums of the greedy evaluation (``es.py:308-322``) before the final mean.
+
+    ``step(state, action, seed)`` is an oracle env step with auto-reset, ``action_of(state)``
+    the greedy action of the shared policy; step t uses counter seed0 + t."""
+    n = state.shape[1]
+    alive = np.ones(n, dtype=bool)
+    fit = np.zeros(n, dtype=F32)
+    for t in range(steps):
+        state, reward, done = step(state, action_of(state), (seed0 + t) & 0xFFFFFFFF)
+        alive = alive & ~done
+        fit = fit + ((reward - F32(1.0)) + F32(eval_bonus)) * alive.astype(F32)
+    return fit

@@ -215,3 +215,34 @@ def rollout_fused(state, theta_pop, hidden, horizon, c, iters=ITERS, alive_bonus
         if not alive.any():
             break
     return total.astype(F32), taken.astype(F32)
+
+
+def evaluate_fused(state, theta, hidden, steps, c, iters=ITERS, eval_bonus=0.0, trig="det"):
+    """Per-env greedy-evaluation sums of one policy ``theta`` (D,) shared by every env, as the
+    fused evaluation kernel runs them: no assist; each env stops at its first fall (which adds
+    nothing), and each standing step adds ((v_x + 1) - 1) + eval_bonus, the reference's
+    ``reward - 1.0 + task.eval_bonus`` with ``reward = v_x + 1`` (``es.py:314-319``,
+    ``legged_np.py:118-121``)."""
+    from .es import unflatten
+
+    n = 3 + c
+    state = np.asarray(state, dtype=F32)
+    p = state.shape[1]
+    theta_pop = np.broadcast_to(np.asarray(theta, dtype=F32), (p, theta.shape[0]))
+    w1, b1, w2, b2 = unflatten(theta_pop, hidden, 5 + 2 * c, 3 * c)
+    q, v = state[:n].copy(), state[n:].copy()
+    alive = np.ones(p, dtype=bool)
+    total = np.zeros(p, dtype=F32)
+    body = Legged(c, iters, mode="f32")
+    bonus = F32(eval_bonus)
+    for _ in range(steps):
+        tq = head_torques(policy_logits(q, v, w1, b1, w2, b2, c, trig), c)
+        nq, nv = body.physics_torques(np.concatenate([q, v]), tq, 0.0)
+        live = alive & ~((nq[1] < FALL_HEIGHT) | (np.abs(nq[2]) > FALL_ANGLE))
+        total = np.where(live, total + (((nv[0] + F32(1.0)) - F32(1.0)) + bonus), total)
+        alive = live
+        q = np.where(alive[None, :], nq, q)
+        v = np.where(alive[None, :], nv, v)
+        if not alive.any():
+            break
+    return total.astype(F32)
