@@ -43,6 +43,8 @@ sample of about `--cpu-seconds` seconds on this host.
   repeats) and peak allocated device memory, for CartPole and Acrobot at
   P = 4,096, H = 32, horizon 500 and legged4 at N = 262,144, H = 64, S = 8,
   horizon 1,000;
+* `step_bodies`: the mass-matrix K-link pendulum (K = 2/4/8/16, RK4 dt 0.02) and the
+  hopper step, N = 65,536, 1,000 graph-replayed steps with uniform {0, 1, 2} actions;
 * `es_evaluate`: the learner's greedy evaluation of the mean policy (es.py:308-322,
   2,048 envs x 500 steps): the fused one-launch kernel against the reference's
   loop (torch mean policy + one env-step launch per iteration); wall time, median
@@ -609,6 +611,51 @@ def bench_aba(dev, steps=1000, n=65536, ks=(4, 16, 64)):
     return out
 
 
+def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
+    """The reference's remaining step modules: the mass-matrix K-link pendulum (RK4, actions
+    drawn per step on the device) and the hopper, graph-replayed like the ABA step."""
+    import torch
+
+    from hipenvs import _lib, cartpole, hopper, pendulum
+
+    P = _lib.ptr
+    out = {}
+    cases = [(f"pendulum_k{k}", 2 * k, 16 * k + 9, k) for k in ks] + [("hopper", 8, 73, None)]
+    for name, rows, bytes_step, k in cases:
+        if k is None:
+            bufs = [hopper.Hopper().reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
+            fn = _lib.lib().hipenvs_hopper_step
+            call = lambda t, s, a: fn(P(bufs[t % 2]), P(a), t + 1, P(bufs[(t + 1) % 2]), P(reward), P(done), n, s)
+        else:
+            bufs = [pendulum.Pendulum(k).reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
+            fn = _lib.lib().hipenvs_pendulum_step
+            call = lambda t, s, a, k=k: fn(k, P(bufs[t % 2]), P(a), t + 1, P(bufs[(t + 1) % 2]), P(reward), P(done),
+                                           n, s)
+        reward = torch.empty(n, device=dev)
+        done = torch.empty(n, dtype=torch.bool, device=dev)
+        actions = torch.empty((steps, n), dtype=torch.int32, device=dev)
+        for t in range(steps):
+            cartpole.sample_actions(n, m=3, seed=1 + t, device=dev, out=actions[t])
+
+        def body(s):
+            for t in range(steps):
+                rc = call(t, s, actions[t])
+                if rc != 0:
+                    raise RuntimeError(f"{name} step failed: {rc}")
+
+        g = capture_graph(dev, body)
+        wall, ev = time_replay(g, 3)
+        launch = ev / steps
+        achieved = bytes_step * n / launch / 1e9
+        out[name] = {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
+                     "bytes_per_env_step": bytes_step,
+                     "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
+        log(f"{name} RK4/substep step N={n}: {n * steps / wall:,.0f} env-steps/s, {launch * 1e6:.2f} us per launch")
+        del g, bufs, actions
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -656,6 +703,7 @@ def main():
         extra["es_generation"] = bench_es_generation(dev, args.repeats, args.legged_n, args.legged_horizon)
         extra["es_evaluate"] = bench_es_evaluate(dev, args.repeats)
         extra["aba_euler"] = bench_aba(dev)
+        extra["step_bodies"] = bench_step_bodies(dev)
 
     cpu = None
     if not args.skip_cpu and args.only in (None, "cartpole"):

@@ -152,6 +152,37 @@ int hipenvs_pendulum_aba_step_euler(int32_t k, const float* state, const float* 
 int hipenvs_pendulum_aba_accelerations(int32_t k, const float* state, const float* torque, float* acc,
                                        int64_t n, hipenvs_stream_t stream);
 
+/* ---- K-link pendulum, mass-matrix form --------------------------------- */
+
+/* One RK4 step of the K-link pendulum with the Lagrangian mass matrix
+ * M_ij = mu_ij cos(th_i - th_j), mu_ij = k - max(i, j), solved by Cholesky at each
+ * stage; otherwise the task of hipenvs_pendulum_aba_step (action, wrap, clip,
+ * termination, reward, all-row reset). k in {1, 2, 3, 4, 8, 16}.
+ * Replaces the `pendulum{K}_step` Metal kernel and pendulum_metal.Pendulum.step
+ * (pendulum_metal.py:59-131, pendulum_np.py:50-82). */
+int hipenvs_pendulum_step(int32_t k, const float* state, const int32_t* action, uint32_t seed,
+                          float* next_state, float* reward, uint8_t* done, int64_t n, hipenvs_stream_t stream);
+
+/* Absolute angular accelerations acc (k, n) from the mass-matrix solve.
+ * Replaces pendulum_np.Pendulum._dsdt's solve (pendulum_np.py:68-79) / the `dsdt<K>`
+ * Metal function (pendulum_metal.py:21-54). */
+int hipenvs_pendulum_accelerations(int32_t k, const float* state, const float* torque, float* acc, int64_t n,
+                                   hipenvs_stream_t stream);
+
+/* ---- Hopper ------------------------------------------------------------- */
+
+/* Fresh states (8, n): the standing pose (0, 1, 0, 0, 0, 0, 0, 0) plus U[+-0.05] on
+ * every row at counter `seed`. Replaces hopper_mlx.Hopper.reset (hopper_mlx.py:19-20). */
+int hipenvs_hopper_reset(float* state, int64_t n, uint32_t seed, hipenvs_stream_t stream);
+
+/* One hopper step: torque (action - 1) * 2 at the hip, four substeps of mass matrix,
+ * 4x4 Cholesky, three solves and the exact single-contact impulse, reward v_x + 1
+ * (0 on a fall), masked reset. state (8, n) q = (x, y, phi, psi) then velocities.
+ * Replaces the `hopper_step` Metal kernel and hopper_metal.Hopper.step
+ * (hopper_metal.py:84-138, hopper_np.py:117-138). */
+int hipenvs_hopper_step(const float* state, const int32_t* action, uint32_t seed, float* next_state,
+                        float* reward, uint8_t* done, int64_t n, hipenvs_stream_t stream);
+
 /* ---- C-legged body with hard contacts ---------------------------------- */
 /* state (2(3+c), n) f32: q = (x, y, phi, psi_1..psi_c), then the velocities.
  * `stand` is the standing pose (2(3+c)) f32 (legged_np.stand_pose). */

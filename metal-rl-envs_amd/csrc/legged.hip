@@ -113,7 +113,11 @@ __device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double 
 // group's LDS rows xs ((2C + 1) x 8 floats). Every value is computed by the same expression
 // as in the one-lane form, so the results are the same bits. Callers keep the group's
 // lanes in one single-wave workgroup, so the barriers order its LDS traffic.
-template <int C, class Div, int kGroup = 0>
+// kHopperSum (C = 1 only) adds the impulse terms as the reference's hopper does,
+// (v_free + M^-1 J_t^T lt) + M^-1 J_n^T ln (hopper_np.py:76), instead of the legged body's
+// v_free + (M^-1 J_t^T lt + M^-1 J_n^T ln) (legged_np.py:95); otherwise the hopper is this
+// body at C = 1 with one sweep.
+template <int C, class Div, int kGroup = 0, bool kHopperSum = false>
 __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
                                         float assist, float assist_damping, Div& div, float* xs = nullptr,
                                         int g = 0) {
@@ -286,10 +290,16 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
   // v = v_free + sum_k M^-1 J_k^T lambda_k; q += h v
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    float s = MiJt[0][i] * lt[0] + MiJn[0][i] * ln[0];
+    float vn;
+    if constexpr (kHopperSum) {
+      static_assert(C == 1, "the hopper has one contact");
+      vn = (vf[i] + MiJt[0][i] * lt[0]) + MiJn[0][i] * ln[0];
+    } else {
+      float s = MiJt[0][i] * lt[0] + MiJn[0][i] * ln[0];
 #pragma unroll
-    for (int k = 1; k < C; ++k) s = s + (MiJt[k][i] * lt[k] + MiJn[k][i] * ln[k]);
-    const float vn = vf[i] + s;
+      for (int k = 1; k < C; ++k) s = s + (MiJt[k][i] * lt[k] + MiJn[k][i] * ln[k]);
+      vn = vf[i] + s;
+    }
     v[i] = vn;
     q[i] = q[i] + H * vn;
   }
@@ -298,7 +308,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
 // One substep dividing through the shared float64 reciprocals; a lane on which a quotient
 // came out subnormal (never met in practice) redoes the substep from its saved state with
 // IEEE division, so the result is always the IEEE one.
-template <int C>
+template <int C, bool kHopperSum = false>
 __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
                                               float assist, float assist_damping) {
   constexpr int N = 3 + C;
@@ -309,7 +319,7 @@ __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + 
     v0[i] = v[i];
   }
   DivRecip fast;
-  substep<C>(q, v, tq, iters, assist, assist_damping, fast);
+  substep<C, DivRecip, 0, kHopperSum>(q, v, tq, iters, assist, assist_damping, fast);
   if (fast.saw_subnormal()) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
@@ -317,7 +327,7 @@ __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + 
       v[i] = v0[i];
     }
     DivIEEE ieee;
-    substep<C>(q, v, tq, iters, assist, assist_damping, ieee);
+    substep<C, DivIEEE, 0, kHopperSum>(q, v, tq, iters, assist, assist_damping, ieee);
   }
 }
 
@@ -470,7 +480,10 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
   }
 }
 
-template <int C>
+// kHopper (C = 1): the reference's hopper step (hopper_metal.py:84-125): torque
+// (a - 1) * TORQUE for any action value, its impulse sum order, and the standing pose
+// (0, L, 0, 0) with zero velocities built in (stand is not read).
+template <int C, bool kHopper = false>
 __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ state,
                                                       const int32_t* __restrict__ action, uint32_t seed,
                                                       const float* __restrict__ stand, int iters, float assist,
@@ -488,23 +501,32 @@ __global__ __launch_bounds__(kBlock) void step_kernel(const float* __restrict__ 
   }
   // leg k gets ((a / 3^k) % 3 - 1) * TORQUE (legged_np.py:51-54)
   int32_t a = stream_load(action + e);
+  if constexpr (kHopper) {
+    tq[0] = (float)(a - 1) * TORQUE;
+  } else {
 #pragma unroll
-  for (int k = 0; k < C; ++k) {
-    tq[k] = (float)(a % 3 - 1) * TORQUE;
-    a /= 3;
+    for (int k = 0; k < C; ++k) {
+      tq[k] = (float)(a % 3 - 1) * TORQUE;
+      a /= 3;
+    }
   }
 #pragma unroll 1
-  for (int s = 0; s < SUBSTEPS; ++s) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
+  for (int s = 0; s < SUBSTEPS; ++s) substep_exact<C, kHopper>(q, v, tq, iters, assist, assist_damping);
   const bool d = fallen<C>(q);
   stream_store(d ? 0.0f : v[0] + 1.0f, reward + e);
   stream_store((uint8_t)(d ? 1 : 0), done + e);
   if (d) {  // fresh draws only on fallen lanes; the reference selects (legged_metal.py:148-152)
     const uint32_t h = env_hash(seed, (uint32_t)e);
 #pragma unroll
-    for (int i = 0; i < N; ++i) q[i] = stand[i] + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
+    for (int i = 0; i < N; ++i) {
+      const float pose = kHopper ? (i == 1 ? 1.0f : 0.0f) : stand[i];  // hopper: y = L = 1
+      q[i] = pose + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
+    }
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-      v[i] = stand[N + i] + uniform_pm(pcg_hash(h + (uint32_t)(N + i) * kRowStride), RESET_BOUND);
+    for (int i = 0; i < N; ++i) {
+      const float pose = kHopper ? 0.0f : stand[N + i];
+      v[i] = pose + uniform_pm(pcg_hash(h + (uint32_t)(N + i) * kRowStride), RESET_BOUND);
+    }
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) next[i * n + e] = q[i];
@@ -522,6 +544,17 @@ __global__ __launch_bounds__(kBlock) void reset_kernel(const float* __restrict__
 #pragma unroll
   for (int i = 0; i < 2 * N; ++i)
     state[i * n + e] = stand[i] + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
+}
+
+// The hopper's reset (hopper_mlx.py:19-20 with the counter RNG of hopper_metal.py:118-120):
+// the standing pose (0, L, 0, 0, 0, 0, 0, 0) plus U[+-0.05] on every row.
+__global__ __launch_bounds__(kBlock) void hopper_reset_kernel(float* __restrict__ state, uint32_t seed, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    state[i * n + e] = (i == 1 ? 1.0f : 0.0f) + uniform_pm(pcg_hash(h + (uint32_t)i * kRowStride), RESET_BOUND);
 }
 
 // Fused ES rollout (legged_rollout_metal.py:19-59). Weight d of member i is
@@ -1199,4 +1232,21 @@ extern "C" int hipenvs_legged_evaluate(int32_t c, int32_t hidden, int32_t iters,
     case 4: return lg::launch_evaluate<4>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
+}
+
+extern "C" int hipenvs_hopper_reset(float* state, int64_t n, uint32_t seed, hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && !state)) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  hipLaunchKernelGGL(lg::hopper_reset_kernel, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), state, seed, n);
+  return launch_status();
+}
+
+extern "C" int hipenvs_hopper_step(const float* state, const int32_t* action, uint32_t seed, float* next_state,
+                                   float* reward, uint8_t* done, int64_t n, hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !action || !next_state || !reward || !done))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  // one exact contact solve per substep: the C = 1 body with one sweep, no assist
+  hipLaunchKernelGGL((lg::step_kernel<1, true>), dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), state, action,
+                     seed, nullptr, 1, 0.0f, 0.0f, next_state, reward, done, n);
+  return launch_status();
 }

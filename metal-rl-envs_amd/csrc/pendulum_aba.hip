@@ -141,6 +141,62 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
   }
 }
 
+// Absolute angular accelerations from the Lagrangian mass-matrix form (pendulum_np.py:68-79,
+// the reference's pendulum_metal.py): M_ij = mu_ij cos(th_i - th_j) and
+// rhs_i = -sum_j mu_ij sin(th_i - th_j) om_j^2 - g mu_ii sin th_i (+ torque at the root),
+// with mu_ij = K - max(i, j) and the differences' cos/sin from K cosines and K sines by the
+// addition formulas, then the Cholesky solve of pendulum_np.py:85-107 (IEEE sqrt and
+// division). Sums run in numpy's order: over j for each row, the factor's rows left to right.
+template <int K>
+__device__ __forceinline__ void mass_matrix_accelerations(const float* th, const float* om, float torque,
+                                                          float* acc) {
+  float c[K], s[K], w2[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    det_sincos(th[i], &s[i], &c[i]);
+    w2[i] = om[i] * om[i];
+  }
+  float L[K][K], y[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    float r = 0.0f;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const float mu = (float)(K - (i > j ? i : j));
+      const float t = (mu * (s[i] * c[j] - c[i] * s[j])) * w2[j];
+      r = (j == 0) ? t : r + t;
+      if (j <= i) L[i][j] = mu * (c[i] * c[j] + s[i] * s[j]);
+    }
+    y[i] = (-r) - (GRAVITY * (float)(K - i)) * s[i];
+  }
+  y[0] = y[0] + torque;
+  // L L^T = M in place, then L y' = y and L^T x = y'
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+#pragma unroll
+    for (int j = 0; j <= i; ++j) {
+      float t = L[i][j];
+#pragma unroll
+      for (int p = 0; p < j; ++p) t = t - L[i][p] * L[j][p];
+      L[i][j] = (i == j) ? sqrtf(t) : t / L[j][j];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    float t = y[i];
+#pragma unroll
+    for (int p = 0; p < i; ++p) t = t - L[i][p] * y[p];
+    y[i] = t / L[i][i];
+  }
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) {
+    float t = y[i];
+#pragma unroll
+    for (int p = i + 1; p < K; ++p) t = t - L[p][i] * acc[p];
+    acc[i] = t / L[i][i];
+  }
+}
+
 // Tip above half the chain's length: -(sum_i cos th_i) > K / 2 (pendulum_np.py:81-82).
 template <int K, int U = K>
 __device__ __forceinline__ bool terminal(const float* th) {
@@ -150,11 +206,21 @@ __device__ __forceinline__ bool terminal(const float* th) {
   return -s > (float)K * 0.5f;
 }
 
-// RK4 at dt 0.02 in place (pendulum_aba_np.py:117-123), stage sums accumulated in numpy's order.
-template <int K, int U = (K <= 16 ? K : 1)>
+// The accelerations of either model: the articulated-body algorithm or the mass matrix.
+template <int K, int U, bool kMassMatrix>
+__device__ __forceinline__ void model_accelerations(const float* th, const float* om, float torque, float* acc) {
+  if constexpr (kMassMatrix)
+    mass_matrix_accelerations<K>(th, om, torque, acc);
+  else
+    accelerations<K, U>(th, om, torque, acc);
+}
+
+// RK4 at dt 0.02 in place (pendulum_aba_np.py:117-123, pendulum_np.py:59-66), stage sums
+// accumulated in numpy's order.
+template <int K, int U = (K <= 16 ? K : 1), bool kMassMatrix = false>
 __device__ __forceinline__ void rk4(float* th, float* om, float torque) {
   float acc[K], t[K], o[K], sth[K], som[K];
-  accelerations<K, U>(th, om, torque, acc);
+  model_accelerations<K, U, kMassMatrix>(th, om, torque, acc);
 #pragma unroll U
   for (int p = 0; p < K; ++p) {
     sth[p] = om[p];
@@ -162,7 +228,7 @@ __device__ __forceinline__ void rk4(float* th, float* om, float torque) {
     t[p] = th[p] + DT_2 * om[p];
     o[p] = om[p] + DT_2 * acc[p];
   }
-  accelerations<K, U>(t, o, torque, acc);
+  model_accelerations<K, U, kMassMatrix>(t, o, torque, acc);
 #pragma unroll U
   for (int p = 0; p < K; ++p) {
     sth[p] = sth[p] + 2.0f * o[p];
@@ -170,7 +236,7 @@ __device__ __forceinline__ void rk4(float* th, float* om, float torque) {
     t[p] = th[p] + DT_2 * o[p];
     o[p] = om[p] + DT_2 * acc[p];
   }
-  accelerations<K, U>(t, o, torque, acc);
+  model_accelerations<K, U, kMassMatrix>(t, o, torque, acc);
 #pragma unroll U
   for (int p = 0; p < K; ++p) {
     sth[p] = sth[p] + 2.0f * o[p];
@@ -178,7 +244,7 @@ __device__ __forceinline__ void rk4(float* th, float* om, float torque) {
     t[p] = th[p] + DT * o[p];
     o[p] = om[p] + DT * acc[p];
   }
-  accelerations<K, U>(t, o, torque, acc);
+  model_accelerations<K, U, kMassMatrix>(t, o, torque, acc);
 #pragma unroll U
   for (int p = 0; p < K; ++p) {
     th[p] = wrap(th[p] + DT_6 * (sth[p] + o[p]));
@@ -230,7 +296,9 @@ __device__ __forceinline__ void store_with_reset(float* __restrict__ next, int64
   for (int p = 0; p < K; ++p) next[(K + p) * n + e] = om[p];
 }
 
-template <int K>
+// kMassMatrix: the reference's pendulum_metal step (the same task with the mass-matrix
+// accelerations, pendulum_metal.py:59-101); otherwise pendulum_aba_metal's.
+template <int K, bool kMassMatrix = false>
 __global__ __launch_bounds__(kBlock) void step_rk4_kernel(const float* __restrict__ state,
                                                           const int32_t* __restrict__ action, uint32_t seed,
                                                           float* __restrict__ next, float* __restrict__ reward,
@@ -240,7 +308,7 @@ __global__ __launch_bounds__(kBlock) void step_rk4_kernel(const float* __restric
   constexpr int U = K <= 16 ? K : 1;
   float th[K], om[K];
   load<K, U>(state, n, e, th, om);
-  rk4<K, U>(th, om, (float)(stream_load(action + e) - 1) * 1.0f);
+  rk4<K, U, kMassMatrix>(th, om, (float)(stream_load(action + e) - 1) * 1.0f);
   const bool d = terminal<K, U>(th);
   store_with_reset<K, false, U>(next, n, e, th, om, d, seed);
   stream_store(d ? 0.0f : -1.0f, reward + e);
@@ -278,6 +346,19 @@ __global__ __launch_bounds__(kBlock) void accelerations_kernel(const float* __re
   for (int p = 0; p < K; ++p) acc_out[p * n + e] = acc[p];
 }
 
+template <int K>
+__global__ __launch_bounds__(kBlock) void mass_matrix_accelerations_kernel(const float* __restrict__ state,
+                                                                           const float* __restrict__ torque,
+                                                                           float* __restrict__ acc_out, int64_t n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float th[K], om[K], acc[K];
+  load<K>(state, n, e, th, om);
+  mass_matrix_accelerations<K>(th, om, torque[e], acc);
+#pragma unroll
+  for (int p = 0; p < K; ++p) acc_out[p * n + e] = acc[p];
+}
+
 template <int K, bool kZeroVelocity>
 __global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state, uint32_t seed, int64_t n) {
   const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -286,7 +367,7 @@ __global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state
   store_with_reset<K, kZeroVelocity>(state, n, e, th, om, true, seed);
 }
 
-enum Op { kRk4, kEulerArray, kEulerRng, kAcc, kReset, kResetZeroVel };
+enum Op { kRk4, kEulerArray, kEulerRng, kAcc, kReset, kResetZeroVel, kMassRk4, kMassAcc };
 
 template <int K>
 int launch(Op op, const float* state, const void* in, uint32_t seed, float* out, float* reward, uint8_t* done,
@@ -312,6 +393,21 @@ int launch(Op op, const float* state, const void* in, uint32_t seed, float* out,
       break;
     case kResetZeroVel:
       hipLaunchKernelGGL((reset_kernel<K, true>), grid, block, 0, s, out, seed, n);
+      break;
+    case kMassRk4:
+      if constexpr (K <= 16) {
+        hipLaunchKernelGGL((step_rk4_kernel<K, true>), grid, block, 0, s, state, (const int32_t*)in, seed, out, reward,
+                           done, n);
+      } else {
+        return HIPENVS_E_UNSUPPORTED;
+      }
+      break;
+    case kMassAcc:
+      if constexpr (K <= 16) {
+        hipLaunchKernelGGL(mass_matrix_accelerations_kernel<K>, grid, block, 0, s, state, (const float*)in, out, n);
+      } else {
+        return HIPENVS_E_UNSUPPORTED;
+      }
       break;
   }
   return launch_status();
@@ -367,4 +463,19 @@ extern "C" int hipenvs_pendulum_aba_accelerations(int32_t k, const float* state,
   if (n < 0 || (n > 0 && (!state || !torque || !acc))) return HIPENVS_E_ARG;
   if (n == 0) return HIPENVS_OK;
   return aba::dispatch(k, aba::kAcc, state, torque, 0, acc, nullptr, nullptr, n, as_stream(stream));
+}
+
+extern "C" int hipenvs_pendulum_step(int32_t k, const float* state, const int32_t* action, uint32_t seed,
+                                     float* next_state, float* reward, uint8_t* done, int64_t n,
+                                     hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !action || !next_state || !reward || !done))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  return aba::dispatch(k, aba::kMassRk4, state, action, seed, next_state, reward, done, n, as_stream(stream));
+}
+
+extern "C" int hipenvs_pendulum_accelerations(int32_t k, const float* state, const float* torque, float* acc,
+                                              int64_t n, hipenvs_stream_t stream) {
+  if (n < 0 || (n > 0 && (!state || !torque || !acc))) return HIPENVS_E_ARG;
+  if (n == 0) return HIPENVS_OK;
+  return aba::dispatch(k, aba::kMassAcc, state, torque, 0, acc, nullptr, nullptr, n, as_stream(stream));
 }

@@ -2,11 +2,13 @@
 
 TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
 
-The hopper itself has no HIP kernel; it is here because the legged body
-reuses its constants and its contact law (``legged_np.py:25``) and because
-the reference pins the legged body by "C = 1 with one sweep is the hopper"
-(test_legged.py:20-26). Follows ``hopper_np.py``: constants (26-34), ``foot``
-(37-40), ``substep`` (43-77), ``contact_impulse`` (80-109), ``Hopper`` (117-138).
+It is the oracle of the HIP hopper step (the reference's ``hopper_metal``),
+and the legged body reuses its constants and its contact law
+(``legged_np.py:25``); the reference pins the legged body by "C = 1 with one
+sweep is the hopper" (test_legged.py:20-26). Follows ``hopper_np.py``:
+constants (26-34), ``foot`` (37-40), ``substep`` (43-77), ``contact_impulse``
+(80-109), ``Hopper`` (117-138), with the counter-RNG reset of
+``hopper_metal.py:118-121``.
 
 ``mode`` selects the arithmetic of ``contact_impulse``: ``"reference"`` is
 literal, including numpy's promotion of ``np.where(slip_p <= 0, 1.0, -1.0)``
@@ -18,7 +20,7 @@ kernel (``legged_metal.py:53-71``) and of the HIP kernels.
 
 import numpy as np
 
-from . import detmath
+from . import detmath, rng
 from .pendulum import cholesky_solve
 
 M_T, I_T, M_F, L = 1.0, 0.1, 0.2, 1.0
@@ -101,7 +103,20 @@ def substep(q, v, torque, mu=MU, mode="reference", trig="numpy"):
 
 
 class Hopper:
-    """``hopper_np.Hopper`` (``hopper_np.py:117-138``) without its RNG reset (physics only)."""
+    """``hopper_np.Hopper`` (``hopper_np.py:117-138``); resets from the counter RNG."""
+
+    def reset(self, n, seed=0):
+        """STAND + U[+-0.05] on every row, row j hashed at j * 0x85EBCA6B (hopper_metal.py:118-120)."""
+        return (STAND[:, None] + rng.reset_rows(seed, n, 8, RESET_BOUND)).astype(np.float32)
+
+    def step(self, state, action, seed, mode="f32", trig="det"):
+        """``hopper_np.py:121-127``: reward forward velocity + 1, 0 on done; fresh state on done."""
+        n = state.shape[1]
+        stepped = self.physics(np.asarray(state, dtype=np.float32), action, mode=mode, trig=trig)
+        done = self.terminated(stepped)
+        next_state = np.where(done[None, :], self.reset(n, seed), stepped).astype(np.float32)
+        reward = np.where(done, 0.0, stepped[4] + 1.0).astype(np.float32)
+        return next_state, reward, done
 
     def physics(self, state, action, mode="reference", trig="numpy"):
         torque = ((np.asarray(action) - 1) * TORQUE).astype(np.float32)

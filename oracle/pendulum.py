@@ -12,7 +12,7 @@ computes, which is how the reference's test_pendulum_aba.py:21-28 uses it.
 
 import numpy as np
 
-from . import detmath
+from . import detmath, rng
 
 F32 = np.float32
 
@@ -106,3 +106,36 @@ def mass_matrix_accelerations_f64(th, om, torque, k):
         rhs[0] += float(torque[e])
         out[:, e] = np.linalg.solve(m, rhs)
     return out
+
+
+class Pendulum:
+    """``pendulum_np.Pendulum`` (``pendulum_np.py:42-82``), the mass-matrix body of the
+    reference's ``pendulum_metal``, with counter-RNG resets (``pendulum_metal.py:94-98``):
+    RK4 at dt 0.02 of ``mass_matrix_dsdt``, wrap, clip, termination, reward -1 / 0."""
+
+    def __init__(self, k, trig="det"):
+        self.k = k
+        self.trig = trig
+
+    def reset(self, n, seed=0):
+        """(2K, n): every row U[+-0.1], row j hashed at j * 0x85EBCA6B."""
+        return rng.reset_rows(seed, n, 2 * self.k, RESET_BOUND)
+
+    def physics(self, state, action):
+        """``pendulum_np.py:59-66``."""
+        state = np.asarray(state, dtype=F32)
+        torque = ((np.asarray(action) - 1) * TORQUE).astype(F32)
+        k1 = mass_matrix_dsdt(state, torque, self.k, self.trig)
+        k2 = mass_matrix_dsdt(state + DT / 2 * k1, torque, self.k, self.trig)
+        k3 = mass_matrix_dsdt(state + DT / 2 * k2, torque, self.k, self.trig)
+        k4 = mass_matrix_dsdt(state + DT * k3, torque, self.k, self.trig)
+        ns = state + DT / 6 * (k1 + 2 * k2 + 2 * k3 + k4)
+        return np.concatenate([wrap(ns[: self.k]), np.clip(ns[self.k:], -MAX_VEL, MAX_VEL)]).astype(F32)
+
+    def step(self, state, action, seed):
+        """``pendulum_np.py:50-57``."""
+        stepped = self.physics(state, action)
+        done = terminated(stepped, self.k, self.trig)
+        next_state = np.where(done[None, :], self.reset(stepped.shape[1], seed), stepped).astype(F32)
+        reward = np.where(done, 0.0, -1.0).astype(F32)
+        return next_state, reward, done
