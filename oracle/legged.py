@@ -60,8 +60,10 @@ def torques(action, c):
     return [((action // 3**k) % 3 - 1).astype(np.float32) * TORQUE for k in range(c)]
 
 
-def substep(q, v, torque, c, iters=ITERS, mu=MU, assist=0.0, mode="f32", trig=None):
-    """One semi-implicit Euler substep with block-PGS contacts; ``legged_np.py:57-97``."""
+def substep(q, v, torque, c, iters=ITERS, mu=MU, assist=0.0, mode="f32", trig=None, hopper_sum=False):
+    """One semi-implicit Euler substep with block-PGS contacts; ``legged_np.py:57-97``.
+    ``hopper_sum`` (C = 1) adds the impulse terms in the hopper's order,
+    ``(v_free + MiJt lt) + MiJn ln`` (``hopper_np.py:76``), as the HIP hopper step does."""
     trig = trig or ("det" if mode == "f32" else "numpy")
     sin_f, cos_f, _ = detmath.trig_functions(trig)
     n = 3 + c
@@ -105,7 +107,11 @@ def substep(q, v, torque, c, iters=ITERS, mu=MU, assist=0.0, mode="f32", trig=No
             wt = w0[k][0] + sum(A[k][l][0] * lt[l] + A[k][l][1] * ln[l] for l in range(c) if l != k)
             wn = w0[k][1] + sum(A[k][l][2] * lt[l] + A[k][l][3] * ln[l] for l in range(c) if l != k)
             lt[k], ln[k] = contact_impulse(A[k][k][0], A[k][k][1], A[k][k][3], wt, wn, depth[k], mu, mode)
-    v_new = np.stack([v_free[i] + sum(MiJt[k][i] * lt[k] + MiJn[k][i] * ln[k] for k in range(c)) for i in range(n)])
+    if hopper_sum:
+        v_new = np.stack([v_free[i] + MiJt[0][i] * lt[0] + MiJn[0][i] * ln[0] for i in range(n)])
+    else:
+        v_new = np.stack([v_free[i] + sum(MiJt[k][i] * lt[k] + MiJn[k][i] * ln[k] for k in range(c))
+                          for i in range(n)])
     return q + H * v_new, v_new
 
 

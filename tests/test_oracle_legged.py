@@ -141,6 +141,19 @@ def test_one_leg_is_the_hopper(mode):
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
 
 
+def test_hopper_is_one_leg_with_the_hoppers_impulse_order():
+    """In float32 the hopper step is the C = 1, one-sweep legged substep exactly once the two
+    impulse terms are added in the hopper's order; the HIP hopper kernel is built that way."""
+    state, action = hopper_states(3000, seed=4)
+    ref = hp.Hopper().physics(state, action, mode="f32", trig="det")
+    q, v = state[:4], state[4:]
+    tq = lg.torques(action, 1)
+    for _ in range(hp.SUBSTEPS):
+        q, v = lg.substep(q, v, tq, 1, iters=1, mode="f32", hopper_sum=True)
+    np.testing.assert_array_equal(np.concatenate([q, v]), ref)
+    assert not np.array_equal(lg.Legged(1, iters=1, mode="f32").physics(state, action), ref)
+
+
 def standing_drift(c, iters, substeps=400, mode="f32"):
     """test_legged.py:29-38."""
     pose = lg.static_pose(c)
