@@ -333,6 +333,175 @@ __global__ __launch_bounds__(kBlock) void step_euler_kernel(const float* __restr
   stream_store((uint8_t)(d ? 1 : 0), done + e);
 }
 
+#ifndef ABA_STAGE_LINKS
+#define ABA_STAGE_LINKS 4
+#endif
+constexpr int kStageLinks = ABA_STAGE_LINKS;  // links whose LDS rows one pass may read ahead
+
+// A (rows, n) float32 array seen by one env through a buffer resource: row r of env e is
+// at byte (r * n + e) * 4, addressed as a per-lane offset e * 4 plus a uniform row offset in
+// a scalar register, so a thread's 2K loads or stores need one address register instead
+// of one per row. Requires rows * n * 4 < 2^31 (checked by the caller); accesses past the
+// array's bytes read 0 and write nothing. 0x00020000 is the gfx9 resource word 3 for a raw
+// 32-bit buffer.
+struct RowBuffer {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t row_bytes, lane_bytes;
+  __device__ RowBuffer(const float* base, int rows, int64_t n, int64_t e)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)(rows * n * 4), 0x00020000)),
+        row_bytes((uint32_t)(n * 4)),
+        lane_bytes((uint32_t)(e * 4)) {}
+  __device__ float load(int r) const {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)lane_bytes, (int)(r * row_bytes), 0));
+  }
+  __device__ void store(int r, float v) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rsrc, (int)lane_bytes, (int)(r * row_bytes), 0);
+  }
+};
+
+// The Euler step for long chains with the per-link state staged by lifetime. The chain's
+// passes keep, per link: cos/sin of the joint angle (all three passes), the link velocity
+// (outward to inward), the velocity-product terms c1, c2 (outward to last), and U, u (inward
+// to last). At K = 64 the step of the generic form holds the input angles and velocities
+// and every per-link array for the whole step, about 790 floats per lane, and spills past
+// the 512 registers. Here the inputs are read as the outward pass consumes them and again
+// for the final update, cos/sin sit in LDS (one 4-byte slot per link and thread, 2 * K * 4 *
+// kBlock bytes per workgroup), and c1, c2 are formed once in the outward pass, so at most
+// about 384 floats per lane are live. Every value is the generic form's, from the same
+// operations in the same order (accelerations, euler, terminal, store_with_reset).
+template <int K, bool kArrayTorque>
+__global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* __restrict__ state,
+                                                                   const float* __restrict__ torque, uint32_t seed,
+                                                                   float* __restrict__ next,
+                                                                   float* __restrict__ reward,
+                                                                   uint8_t* __restrict__ done, int64_t n) {
+  __shared__ float trig_lds[2 * K * kBlock];
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float* sn_l = trig_lds + threadIdx.x;          // sin of joint i at sn_l[i * kBlock]
+  float* cs_l = trig_lds + K * kBlock + threadIdx.x;
+  const float tq = kArrayTorque ? stream_load(torque + e)
+                                : uniform_pm(pcg_hash(env_hash(seed, (uint32_t)e) + kTorqueOffset), 1.0f);
+  float vw[K], vx[K], vy[K], c1[K], c2[K], U0[K], U1[K], U2[K], uu[K], acc[K];
+  const RowBuffer in(state, 2 * K, n, e);
+  // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
+  {
+    float w = 0.0f, x = 0.0f, y = 0.0f, th_prev = 0.0f, om_prev = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const float th_i = in.load(i), om_i = in.load(K + i);
+      const float q = (i == 0) ? th_i : th_i - th_prev;
+      const float qd = (i == 0) ? om_i : om_i - om_prev;
+      float sn, cs;
+      det_sincos(q, &sn, &cs);
+      sn_l[i * kBlock] = sn;
+      cs_l[i * kBlock] = cs;
+      const float xy = (i == 0) ? (y + w * 0.0f) : (y + w);
+      const float nw = w + qd;
+      const float nx = cs * x + sn * xy;
+      const float ny = (-sn) * x + cs * xy;
+      vw[i] = nw;
+      vx[i] = nx;
+      vy[i] = ny;
+      c1[i] = qd * ny;
+      c2[i] = (-qd) * nx;
+      w = nw;
+      x = nx;
+      y = ny;
+      th_prev = th_i;
+      om_prev = om_i;
+    }
+  }
+  asm volatile("" ::: "memory");  // each pass reads its LDS rows in its own order, not hoisted into the last
+  // inward: articulated inertia and bias folded into the parent (pendulum_aba_np.py:51-82)
+  {
+    float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
+    float P0, P1, P2;
+    own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
+#pragma unroll
+    for (int i = K - 1; i >= 0; --i) {
+      U0[i] = A0;
+      U1[i] = A1;
+      U2[i] = A2;
+      uu[i] = (i == 0 ? tq : 0.0f) - P0;
+      if (i == 0) break;
+      const float D = A0;
+      const float I0 = A0 - (A0 * A0) / D, I1 = A1 - (A0 * A1) / D, I2 = A2 - (A0 * A2) / D;
+      const float I3 = A3 - (A1 * A1) / D, I4 = A4 - (A1 * A2) / D, I5 = A5 - (A2 * A2) / D;
+      const float Iac0 = I1 * c1[i] + I2 * c2[i];
+      const float Iac1 = I3 * c1[i] + I4 * c2[i];
+      const float Iac2 = I4 * c1[i] + I5 * c2[i];
+      const float g = uu[i] / D;
+      const float pa0 = (P0 + Iac0) + A0 * g;
+      const float pa1 = (P1 + Iac1) + A1 * g;
+      const float pa2 = (P2 + Iac2) + A2 * g;
+      const float c = cs_l[i * kBlock], s = sn_l[i * kBlock];
+      const float B00 = (I0 + I1 * s) + I2 * c, B01 = I1 * c - I2 * s, B02 = I1 * s + I2 * c;
+      const float B10 = (I1 + I3 * s) + I4 * c, B11 = I3 * c - I4 * s, B12 = I3 * s + I4 * c;
+      const float B20 = (I2 + I4 * s) + I5 * c, B21 = I4 * c - I5 * s, B22 = I4 * s + I5 * c;
+      A0 = 1.0f + ((B00 + s * B10) + c * B20);
+      A1 = (B01 + s * B11) + c * B21;
+      A2 = 1.0f + ((B02 + s * B12) + c * B22);
+      A3 = 1.0f + (c * B11 - s * B21);
+      A4 = c * B12 - s * B22;
+      A5 = 1.0f + (s * B12 + c * B22);
+      float pp0, pp1, pp2;
+      own_bias(vw[i - 1], vx[i - 1], vy[i - 1], pp0, pp1, pp2);
+      P0 = ((pp0 + pa0) + s * pa1) + c * pa2;
+      P1 = (pp1 + c * pa1) - s * pa2;
+      P2 = (pp2 + s * pa1) + c * pa2;
+      if ((i & (kStageLinks - 1)) == 0) asm volatile("" ::: "memory");  // LDS reads kStageLinks links ahead at most
+    }
+  }
+  asm volatile("" ::: "memory");
+  // outward: accelerations from a base accelerating at -g (pendulum_aba_np.py:83-99)
+  {
+    float aw = 0.0f, ax = -GRAVITY, ay = 0.0f, run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const float c = cs_l[i * kBlock], s = sn_l[i * kBlock];
+      const float xy = (i == 0) ? (ay + aw * 0.0f) : (ay + aw);
+      const float ap0 = aw;
+      const float ap1 = (c * ax + s * xy) + c1[i];
+      const float ap2 = ((-s) * ax + c * xy) + c2[i];
+      const float qdd = (uu[i] - ((U0[i] * ap0 + U1[i] * ap1) + U2[i] * ap2)) / U0[i];
+      aw = ap0 + qdd;
+      ax = ap1;
+      ay = ap2;
+      run = run + qdd;
+      acc[i] = run;
+      if ((i & (kStageLinks - 1)) == kStageLinks - 1) asm volatile("" ::: "memory");
+    }
+  }
+  // The final update reads the inputs again. The reads go through a copy of the pointer
+  // that the compiler cannot see through, so they are not hoisted above the passes (the
+  // input is read-only, and a plain memory barrier does not hold its loads back).
+  const float* again = state;
+  asm volatile("" : "+s"(again)::"memory");
+  const RowBuffer in2(again, 2 * K, n, e), out(next, 2 * K, n, e);
+  // semi-implicit Euler, wrap, clip, termination, masked reset
+  float cos_sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    const float om_new = in2.load(K + p) + DT_EULER * acc[p];
+    const float th_new = wrap(in2.load(p) + DT_EULER * om_new);
+    out.store(p, th_new);
+    out.store(K + p, clip(om_new, -MAX_VEL, MAX_VEL));
+    cos_sum = (p == 0) ? det_cos(th_new) : cos_sum + det_cos(th_new);
+  }
+  const bool d = -cos_sum > (float)K * 0.5f;
+  if (d) {  // angles U[+-0.1], zero velocities, overwriting the stepped state
+    const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+    for (int p = 0; p < K; ++p) {
+      out.store(p, uniform_pm(pcg_hash(h + (uint32_t)p * kRowStride), RESET_BOUND));
+      out.store(K + p, 0.0f);
+    }
+  }
+  stream_store(d ? 0.0f : -1.0f, reward + e);
+  stream_store((uint8_t)(d ? 1 : 0), done + e);
+}
+
 template <int K>
 __global__ __launch_bounds__(kBlock) void accelerations_kernel(const float* __restrict__ state,
                                                                const float* __restrict__ torque,
@@ -367,6 +536,12 @@ __global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state
   store_with_reset<K, kZeroVelocity>(state, n, e, th, om, true, seed);
 }
 
+// Chains at least this long take the staged Euler kernel.
+#ifndef ABA_STAGED_EULER_MIN_K
+#define ABA_STAGED_EULER_MIN_K 64
+#endif
+constexpr int kStagedEulerMinK = ABA_STAGED_EULER_MIN_K;
+
 enum Op { kRk4, kEulerArray, kEulerRng, kAcc, kReset, kResetZeroVel, kMassRk4, kMassAcc };
 
 template <int K>
@@ -378,13 +553,26 @@ int launch(Op op, const float* state, const void* in, uint32_t seed, float* out,
       hipLaunchKernelGGL(step_rk4_kernel<K>, grid, block, 0, s, state, (const int32_t*)in, seed, out, reward, done, n);
       break;
     case kEulerArray:
-      hipLaunchKernelGGL((step_euler_kernel<K, true>), grid, block, 0, s, state, (const float*)in, seed, out, reward,
-                         done, n);
+    case kEulerRng: {
+      // the staged kernel addresses the (2K, n) arrays with 32-bit byte offsets
+      const bool staged = K >= kStagedEulerMinK && (int64_t)2 * K * n * 4 < ((int64_t)1 << 31);
+      const bool array = op == kEulerArray;
+      if constexpr (K >= kStagedEulerMinK) {
+        if (staged && array)
+          hipLaunchKernelGGL((step_euler_staged_kernel<K, true>), grid, block, 0, s, state, (const float*)in, seed,
+                             out, reward, done, n);
+        if (staged && !array)
+          hipLaunchKernelGGL((step_euler_staged_kernel<K, false>), grid, block, 0, s, state, (const float*)in, seed,
+                             out, reward, done, n);
+      }
+      if (!staged && array)
+        hipLaunchKernelGGL((step_euler_kernel<K, true>), grid, block, 0, s, state, (const float*)in, seed, out, reward,
+                           done, n);
+      if (!staged && !array)
+        hipLaunchKernelGGL((step_euler_kernel<K, false>), grid, block, 0, s, state, (const float*)in, seed, out,
+                           reward, done, n);
       break;
-    case kEulerRng:
-      hipLaunchKernelGGL((step_euler_kernel<K, false>), grid, block, 0, s, state, (const float*)in, seed, out, reward,
-                         done, n);
-      break;
+    }
     case kAcc:
       hipLaunchKernelGGL(accelerations_kernel<K>, grid, block, 0, s, state, (const float*)in, out, n);
       break;
