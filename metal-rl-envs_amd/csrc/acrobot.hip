@@ -166,6 +166,63 @@ __global__ __launch_bounds__(64) void rollout_kernel(const float* __restrict__ s
 constexpr int kRolloutLanes = 16;
 constexpr int kRolloutMembers = 64 / kRolloutLanes;
 
+// The group's physics, with the transcendentals and the two quotients by d1 spread over the
+// group's lanes: lanes 0, 1, 2 evaluate one det_sincos each (one instruction stream for the
+// three) and every lane of the 16-lane group (one DPP row) receives the results by row
+// broadcast. Each value is the single-lane function's on the same argument, so the bits
+// are those of dsdt/rk4/terminal.
+template <int L>
+__device__ __forceinline__ float group_bcast(float v) {  // DPP row_newbcast:L
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
+}
+
+struct GroupTrig {
+  float sin_a, cos_a, sin_b, cos_b, cos_ab;  // theta1, theta2, theta2 + theta1
+};
+
+__device__ __forceinline__ GroupTrig group_trig(const S4& s, int g) {
+  const float x = (g == 1) ? s.b : (g == 2) ? (s.b + s.a) : s.a;
+  float sn, cs;
+  det_sincos(x, &sn, &cs);
+  return GroupTrig{group_bcast<0>(sn), group_bcast<0>(cs), group_bcast<1>(sn), group_bcast<1>(cs),
+                   group_bcast<2>(cs)};
+}
+
+__device__ __forceinline__ S4 dsdt_group(const S4& s, float torque, int g) {
+  const float x = (g == 1) ? ((s.a + s.b) - HALF_PI) : (g == 2) ? (s.a - HALF_PI) : s.b;
+  float sn, cs;
+  det_sincos(x, &sn, &cs);
+  const float s2 = group_bcast<0>(sn), c2 = group_bcast<0>(cs);
+  const float d1 = ((D1_C0 + (D1_C1 + c2)) + 1.0f) + 1.0f;
+  const float d2 = (D2_C0 + D2_C1 * c2) + 1.0f;
+  const float phi2 = PHI2_C * group_bcast<1>(cs);
+  const float t1 = (PHI1_A * (s.d * s.d)) * s2;
+  const float t2 = (s.d * s.c) * s2;
+  const float t3 = PHI1_C * group_bcast<2>(cs);
+  const float phi1 = ((t1 - t2) + t3) + phi2;
+  const float q = ((g == 1) ? d2 * d2 : d2) / d1;  // lane 0: d2 / d1, lane 1: (d2 * d2) / d1
+  const float num = ((torque + group_bcast<0>(q) * phi1) - (DD2_C * (s.c * s.c)) * s2) - phi2;
+  const float den = DEN_C - group_bcast<1>(q);
+  const float dd2 = num / den;
+  const float dd1 = (-((d2 * dd2) + phi1)) / d1;
+  return S4{s.c, s.d, dd1, dd2};
+}
+
+__device__ __forceinline__ void rk4_group(S4& s, float torque, int g) {
+  const S4 k1 = dsdt_group(s, torque, g);
+  const S4 k2 = dsdt_group(S4{s.a + DT_2 * k1.a, s.b + DT_2 * k1.b, s.c + DT_2 * k1.c, s.d + DT_2 * k1.d}, torque, g);
+  const S4 k3 = dsdt_group(S4{s.a + DT_2 * k2.a, s.b + DT_2 * k2.b, s.c + DT_2 * k2.c, s.d + DT_2 * k2.d}, torque, g);
+  const S4 k4 = dsdt_group(S4{s.a + DT * k3.a, s.b + DT * k3.b, s.c + DT * k3.c, s.d + DT * k3.d}, torque, g);
+  const float na = s.a + DT_6 * (((k1.a + 2.0f * k2.a) + 2.0f * k3.a) + k4.a);
+  const float nb = s.b + DT_6 * (((k1.b + 2.0f * k2.b) + 2.0f * k3.b) + k4.b);
+  const float nc = s.c + DT_6 * (((k1.c + 2.0f * k2.c) + 2.0f * k3.c) + k4.c);
+  const float nd = s.d + DT_6 * (((k1.d + 2.0f * k2.d) + 2.0f * k3.d) + k4.d);
+  s.a = wrap(na);
+  s.b = wrap(nb);
+  s.c = clip(nc, -MAX_VEL_1, MAX_VEL_1);
+  s.d = clip(nd, -MAX_VEL_2, MAX_VEL_2);
+}
+
 template <int H>
 __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restrict__ state,
                                                            const float* __restrict__ theta, int64_t member_stride,
@@ -198,10 +255,13 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
   float steps = 0.0f;
   int32_t t = 0;
   alive = alive && horizon > 0;
-  while (__any(alive)) {  // every lane steps, so the barriers stay uniform
+  GroupTrig tr = group_trig(s, g);  // the observation's trig; after each step also the termination's
+  while (__any(alive)) {  // every lane steps, so the barriers and row broadcasts stay uniform
     float ob[6];
-    det_sincos(s.a, &ob[1], &ob[0]);
-    det_sincos(s.b, &ob[3], &ob[2]);
+    ob[0] = tr.cos_a;
+    ob[1] = tr.sin_a;
+    ob[2] = tr.cos_b;
+    ob[3] = tr.sin_b;
     ob[4] = s.c;
     ob[5] = s.d;
 #pragma unroll
@@ -225,8 +285,9 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
     float torque = -1.0f, best = l0;
     if (l1 > best) { torque = 0.0f; best = l1; }
     if (l2 > best) { torque = 1.0f; }
-    rk4(s, torque);
-    const bool done = terminal(s);
+    rk4_group(s, torque, g);
+    tr = group_trig(s, g);
+    const bool done = (-tr.cos_a) - tr.cos_ab > 1.0f;  // terminal(s)
     if (alive) {
       if (done) {
         alive = false;
