@@ -32,9 +32,12 @@ sample of about `--cpu-seconds` seconds on this host.
   the reference's literal arithmetic: einsum policy + legged_np step) timed
   on a bounded sample of steps at the same N;
 * `cartpole_fused_k32`: the K = 32 fused CartPole step, in-kernel and array actions;
-* `es_config2`: CartPole and Acrobot fused ES rollouts, P = 4,096, H = 32, horizon 500;
+* `es_config2`: CartPole and Acrobot fused ES rollouts, P = 4,096, H = 32, horizon 500,
+  with the reference's numpy ES loop (all members stepped every iteration) timed beside
+  them in member-steps/s, to compare with the GPU's P x horizon rate;
 * `aba_euler`: the K-link pendulum, semi-implicit Euler dt 0.01, N = 65,536,
-  K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B);
+  K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B) and the
+  numpy ABA Euler step timed beside it;
 * `es_generation`: one whole ES generation (noise, rollout, centered ranks,
   update) two ways: "materialised" is the reference's generation (es.py:218-227)
   in torch around the fused rollout ((P/2, D) randn, concatenated noise,
@@ -417,6 +420,65 @@ def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
     return out
 
 
+def cpu_baseline_es(task, seconds, p=4096, hidden=32):
+    """The reference's numpy ES path for config 2 (es.py:174-193 with the numpy backend):
+    every iteration runs the einsum policy (es.py:167-171) and the numpy env step over all P
+    members. Returns member-steps per second (P x iterations / s) and the iterations timed."""
+    import numpy as np
+
+    from oracle import acrobot as oa
+    from oracle import cartpole as oc
+    from oracle import es as oes
+
+    obs_dim, n_out, env = (4, 2, oc) if task == "cartpole" else (6, 3, oa)
+    r = np.random.default_rng(0)
+    d = oes.n_params(hidden, obs_dim, n_out)
+    theta0 = r.standard_normal(d, dtype=np.float32) * np.float32(0.1)
+    half = r.standard_normal((p // 2, d), dtype=np.float32)
+    w1, b1, w2, b2 = oes.unflatten(theta0[None, :] + np.float32(0.1) * np.concatenate([half, -half]), hidden,
+                                   obs_dim, n_out)
+    state = env.reset(p, seed=0)
+
+    def obs(st):
+        if task == "cartpole":
+            return st.T
+        th1, th2, dth1, dth2 = st
+        return np.stack([np.cos(th1), np.sin(th1), np.cos(th2), np.sin(th2), dth1, dth2], axis=1)
+
+    def one(t, st):
+        h = np.tanh(np.einsum("pi,pih->ph", obs(st), w1) + b1)
+        action = np.argmax(np.einsum("ph,pho->po", h, w2) + b2, axis=-1).astype(np.int32)
+        return env.step(st, action, t, trig="numpy")[0]
+
+    state = one(1, state)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        state = one(steps + 2, state)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return p * steps / el, steps
+
+
+def cpu_baseline_aba(k, seconds, n=65536):
+    """The numpy ABA (the oracle's restatement of pendulum_aba_np.aba_accelerations with np.sin/
+    np.cos) stepped by semi-implicit Euler at N envs, one process; env-steps per second."""
+    from oracle import pendulum_aba as opa
+
+    body = opa.Pendulum(k, trig="numpy")
+    state = body.reset_euler(n, seed=0)
+    state = body.step_euler(state, None, 1)[0]
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        state = body.step_euler(state, None, steps + 2)[0]
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return n * steps / el, steps
+
+
 def cpu_baseline_legged(n, seconds, c=4, hidden=64, sweeps=8):
     """The reference's numpy ES path at N members: einsum policy (es.py:167-171), per-leg
     argmax (es.py:86-93), legged_np step in its literal arithmetic; steps per second."""
@@ -700,9 +762,27 @@ def main():
         extra["legged4_es_rollout"] = legged
     if args.only is None:
         extra["es_config2"] = bench_es_config2(dev, args.repeats)
+        if not args.skip_cpu:
+            for task in ("cartpole", "acrobot"):
+                rate, its = cpu_baseline_es(task, 2.0)
+                rec = extra["es_config2"][task]
+                rec["cpu_baseline"] = {"value": rate, "unit": "member-steps/s", "cores": 1, "kind": "port",
+                                       "sample": f"numpy ES loop (einsum policy + numpy {task} step over all 4,096 "
+                                                 f"members per iteration, es.py:174-193), {its} iterations"}
+                rec["speedup_p_x_horizon_vs_cpu"] = rec["p_x_horizon_per_s"] / rate
+                log(f"ES {task} numpy loop: {rate:,.0f} member-steps/s -> GPU P x H rate "
+                    f"{rec['speedup_p_x_horizon_vs_cpu']:,.0f}x")
         extra["es_generation"] = bench_es_generation(dev, args.repeats, args.legged_n, args.legged_horizon)
         extra["es_evaluate"] = bench_es_evaluate(dev, args.repeats)
         extra["aba_euler"] = bench_aba(dev)
+        if not args.skip_cpu:
+            for k, rec in extra["aba_euler"].items():
+                rate, its = cpu_baseline_aba(int(k), 1.5)
+                rec["cpu_baseline"] = {"value": rate, "unit": "env-steps/s", "cores": 1, "kind": "port",
+                                       "sample": f"numpy ABA Euler step (np.sin/np.cos) at N=65,536, K={k}, "
+                                                 f"{its} steps"}
+                rec["speedup_vs_cpu"] = rec["env_steps_per_s"] / rate
+                log(f"ABA K={k} numpy: {rate:,.0f} env-steps/s -> GPU {rec['speedup_vs_cpu']:,.0f}x")
         extra["step_bodies"] = bench_step_bodies(dev)
 
     cpu = None
