@@ -32,7 +32,7 @@ constexpr double INV_TOTAL_MASS = 1.0 / (double)TOTAL_MASS;  // for div_const(x,
 __device__ __forceinline__ bool advance(float& x, float& xd, float& th, float& thd, int32_t action) {
   const float force = (action == 1) ? FORCE_MAG : -FORCE_MAG;
   float s, c;
-  det_sincos(th, &s, &c);
+  det_sincos_near_zero(th, &s, &c);  // the pole angle stays within +-0.78 but for a terminating step
   const float temp = div_const(force + (POLE_MASS_LENGTH * (thd * thd)) * s, INV_TOTAL_MASS);
   const float theta_acc = (GRAVITY * s - c * temp) /
                           (HALF_POLE_LENGTH * (FOUR_THIRDS - div_const(POLE_MASS * (c * c), INV_TOTAL_MASS)));

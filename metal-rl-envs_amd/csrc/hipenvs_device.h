@@ -77,6 +77,20 @@ constexpr float E2 = 0x1p-1f, E3 = 0x1.555556p-3f, E4 = 0x1.555556p-5f, E5 = 0x1
 constexpr float TANH_CLAMP = 10.0f;
 }  // namespace dm
 
+// sin and cos of a reduced argument r, |r| <= pi/4, by the Taylor polynomials.
+__device__ __forceinline__ void sincos_poly(float r, float* sin_out, float* cos_out) {
+  const float z = r * r;
+  float sp = dm::S7 + z * dm::S9;
+  sp = dm::S5 + z * sp;
+  sp = dm::S3 + z * sp;
+  *sin_out = r + (r * z) * sp;
+  float cp = dm::C8 + z * dm::C10;
+  cp = dm::C6 + z * cp;
+  cp = dm::C4 + z * cp;
+  cp = dm::C2 + z * cp;
+  *cos_out = 1.0f + z * cp;
+}
+
 __device__ __forceinline__ void det_sincos(float x, float* sin_out, float* cos_out) {
   // float32 reduction, computed for every lane on an argument clamped into its range (so
   // no branch precedes it and independent work can overlap the loads that feed x) ...
@@ -92,20 +106,24 @@ __device__ __forceinline__ void det_sincos(float x, float* sin_out, float* cos_o
     const double qd = kd - 4.0 * floor(kd * 0.25);
     q = (qd >= 0.0 && qd < 4.0) ? ((int)qd & 3) : 0;  // inf/NaN: quadrant 0, result NaN
   }
-  const float z = r * r;
-  float sp = dm::S7 + z * dm::S9;
-  sp = dm::S5 + z * sp;
-  sp = dm::S3 + z * sp;
-  const float s = r + (r * z) * sp;
-  float cp = dm::C8 + z * dm::C10;
-  cp = dm::C6 + z * cp;
-  cp = dm::C4 + z * cp;
-  cp = dm::C2 + z * cp;
-  const float c = 1.0f + z * cp;
+  float s, c;
+  sincos_poly(r, &s, &c);
   const float a = (q & 1) ? c : s;
   const float b = (q & 1) ? s : c;
   *sin_out = (q & 2) ? -a : a;
   *cos_out = ((q + 1) & 2) ? -b : b;
+}
+
+// det_sincos for arguments that are usually near zero (CartPole's pole angle). When every
+// active lane of the wave has |x| <= 0.78, rint(x * 2/pi) is 0 on every lane, the reduction
+// returns x itself (a zero of either sign gives the same sin and cos), and the quadrant is
+// 0, so the polynomial alone returns det_sincos's bits. Otherwise the wave takes det_sincos.
+__device__ __forceinline__ void det_sincos_near_zero(float x, float* sin_out, float* cos_out) {
+  if (__all(fabsf(x) <= 0.78f)) {
+    sincos_poly(x, sin_out, cos_out);
+  } else {
+    det_sincos(x, sin_out, cos_out);
+  }
 }
 
 __device__ __forceinline__ float det_sin(float x) {
