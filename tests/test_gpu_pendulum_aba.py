@@ -96,3 +96,23 @@ def test_resets_and_lazy_chain(dev):
         state, _, _ = p.step(state, torch.randint(0, 3, (n,), device=dev, dtype=torch.int32))
     out = to_np(state)
     assert np.isfinite(out).all() and np.all(np.abs(out[:8]) <= np.pi)
+
+
+def test_k64_euler_full_size_with_terminations(dev):
+    """The staged K = 64 Euler kernel at the benchmark's N = 65,536: one step bit for bit
+    against the oracle, with chains pointing up (terminated, reset to angles U[+-0.1] and
+    zero velocities) in some columns and random chains elsewhere."""
+    from hipenvs import pendulum_aba
+
+    k, n = 64, 65_536
+    state, _ = random_state(k, n, seed=64)
+    state[:k, ::97] = np.float32(np.pi)  # tip at height 64 > 32: these terminate
+    torque = rng.torque_uniform(11, n)
+    p = pendulum_aba.Pendulum(k)
+    p.reseed(10)
+    ns, rew, done = p.step_euler(torch.from_numpy(state).to(dev), torch.from_numpy(torque).to(dev))
+    ens, erew, edone = oaba.Pendulum(k).step_euler(state, torque, seed=11)
+    assert edone.sum() >= n // 97
+    np.testing.assert_array_equal(to_np(done), edone)
+    np.testing.assert_array_equal(to_np(rew), erew)
+    np.testing.assert_array_equal(to_np(ns), ens)
