@@ -46,8 +46,10 @@ sample of about `--cpu-seconds` seconds on this host.
   repeats) and peak allocated device memory, for CartPole and Acrobot at
   P = 4,096, H = 32, horizon 500 and legged4 at N = 262,144, H = 64, S = 8,
   horizon 1,000;
-* `step_bodies`: the mass-matrix K-link pendulum (K = 2/4/8/16, RK4 dt 0.02) and the
-  hopper step, N = 65,536, 1,000 graph-replayed steps with uniform {0, 1, 2} actions;
+* `step_bodies`: single-step kernels graph-replayed for 1,000 steps with actions drawn on
+  the device: the mass-matrix K-link pendulum (K = 2/4/8/16, RK4 dt 0.02) and the hopper at
+  N = 65,536; the Acrobot step at N = 262,144; the legged C = 4 step with 8 sweeps at
+  N = 65,536 (uniform actions in [0, 81)) -- the reference's own step benchmarks' shapes;
 * `es_evaluate`: the learner's greedy evaluation of the mean policy (es.py:308-322,
   2,048 envs x 500 steps): the fused one-launch kernel against the reference's
   loop (torch mean policy + one env-step launch per iteration); wall time, median
@@ -678,16 +680,29 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
     drawn per step on the device) and the hopper, graph-replayed like the ABA step."""
     import torch
 
-    from hipenvs import _lib, cartpole, hopper, pendulum
+    from hipenvs import _lib, acrobot, cartpole, hopper, legged, pendulum
 
     P = _lib.ptr
     out = {}
-    cases = [(f"pendulum_k{k}", 2 * k, 16 * k + 9, k) for k in ks] + [("hopper", 8, 73, None)]
-    for name, rows, bytes_step, k in cases:
-        if k is None:
+    cases = [(f"pendulum_k{k}", 2 * k, 16 * k + 9, k, n) for k in ks] + [("hopper", 8, 73, "hopper", n),
+                                                                         ("acrobot", 4, 41, "acrobot", 262144),
+                                                                         ("legged4_s8", 14, 121, "legged", n)]
+    for name, rows, bytes_step, k, n in cases:
+        if k == "hopper":
             bufs = [hopper.Hopper().reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
             fn = _lib.lib().hipenvs_hopper_step
             call = lambda t, s, a: fn(P(bufs[t % 2]), P(a), t + 1, P(bufs[(t + 1) % 2]), P(reward), P(done), n, s)
+        elif k == "acrobot":
+            bufs = [acrobot.reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
+            fn = _lib.lib().hipenvs_acrobot_step
+            call = lambda t, s, a: fn(P(bufs[t % 2]), P(a), t + 1, P(bufs[(t + 1) % 2]), P(reward), P(done), n, s)
+        elif k == "legged":
+            body = legged.Legged(4, 8)
+            bufs = [body.reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
+            stand = body.stand_on(dev)
+            fn = _lib.lib().hipenvs_legged_step
+            call = lambda t, s, a: fn(4, 8, 0.0, P(bufs[t % 2]), P(a), t + 1, P(stand), P(bufs[(t + 1) % 2]), P(reward),
+                                      P(done), n, s)
         else:
             bufs = [pendulum.Pendulum(k).reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
             fn = _lib.lib().hipenvs_pendulum_step
@@ -696,8 +711,9 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
         reward = torch.empty(n, device=dev)
         done = torch.empty(n, dtype=torch.bool, device=dev)
         actions = torch.empty((steps, n), dtype=torch.int32, device=dev)
+        n_actions = 81 if k == "legged" else 3
         for t in range(steps):
-            cartpole.sample_actions(n, m=3, seed=1 + t, device=dev, out=actions[t])
+            cartpole.sample_actions(n, m=n_actions, seed=1 + t, device=dev, out=actions[t])
 
         def body(s):
             for t in range(steps):
@@ -713,7 +729,7 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
                      "bytes_per_env_step": bytes_step,
                      "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
-        log(f"{name} RK4/substep step N={n}: {n * steps / wall:,.0f} env-steps/s, {launch * 1e6:.2f} us per launch")
+        log(f"{name} step N={n}: {n * steps / wall:,.0f} env-steps/s, {launch * 1e6:.2f} us per launch")
         del g, bufs, actions
     return out
 
