@@ -367,6 +367,12 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
 #ifndef LEGGED_ROLLOUT_MIN_WAVES
 #define LEGGED_ROLLOUT_MIN_WAVES 1
 #endif
+// The same for the first chunk of the compacting schedule, which streams every member's
+// weights from HBM. Two waves per SIMD there (256 registers, 32 spilled) made the whole
+// rollout slower (64.4 -> 94.3 ms at the ES benchmark's shape), so one wave keeps them all.
+#ifndef LEGGED_FIRST_CHUNK_MIN_WAVES
+#define LEGGED_FIRST_CHUNK_MIN_WAVES 1
+#endif
 
 // POLICY_UNROLL hidden units per policy loop iteration bounds how many of the member's
 // weight loads are in flight at once.
@@ -739,7 +745,7 @@ __global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t ca
 }
 
 template <int C, int HID, bool kFirst>
-__global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_kernel(const float* __restrict__ state0,
+__global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_kernel(const float* __restrict__ state0,
                                                            const float* __restrict__ theta0, int64_t p,
                                                            Packed src, Packed dst, int64_t cap,
                                                            int32_t chunk_steps, int32_t horizon, int iters,
