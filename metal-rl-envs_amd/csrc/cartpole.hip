@@ -223,9 +223,10 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
     __syncthreads();
     const float l0 = xl[0], l1 = xl[1];
     __syncthreads();  // the group's rows are read before the next step writes them
-    const bool done = advance(x, xd, th, thd, (l1 > l0) ? 1 : 0);
+    // only live members step (the physics has no barrier), so the near-zero sin/cos vote
+    // sees the live pole angles alone
     if (alive) {
-      if (done) {
+      if (advance(x, xd, th, thd, (l1 > l0) ? 1 : 0)) {
         alive = false;
       } else {
         survived += 1.0f;
