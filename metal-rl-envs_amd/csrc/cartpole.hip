@@ -29,10 +29,12 @@ constexpr double INV_TOTAL_MASS = 1.0 / (double)TOTAL_MASS;  // for div_const(x,
 
 // One explicit-Euler step in place; returns the termination flag.
 // cartpole_np.py:58-83, each line evaluated in numpy's order.
-__device__ __forceinline__ bool advance(float& x, float& xd, float& th, float& thd, int32_t action) {
+// `exact` false marks a lane whose results are discarded (see det_sincos_near_zero).
+__device__ __forceinline__ bool advance(float& x, float& xd, float& th, float& thd, int32_t action,
+                                        bool exact = true) {
   const float force = (action == 1) ? FORCE_MAG : -FORCE_MAG;
   float s, c;
-  det_sincos_near_zero(th, &s, &c);  // the pole angle stays within +-0.78 but for a terminating step
+  det_sincos_near_zero(th, &s, &c, exact);  // the pole angle stays within +-0.78 but for a terminating step
   const float temp = div_const(force + (POLE_MASS_LENGTH * (thd * thd)) * s, INV_TOTAL_MASS);
   const float theta_acc = (GRAVITY * s - c * temp) /
                           (HALF_POLE_LENGTH * (FOUR_THIRDS - div_const(POLE_MASS * (c * c), INV_TOTAL_MASS)));
@@ -223,10 +225,11 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
     __syncthreads();
     const float l0 = xl[0], l1 = xl[1];
     __syncthreads();  // the group's rows are read before the next step writes them
-    // only live members step (the physics has no barrier), so the near-zero sin/cos vote
-    // sees the live pole angles alone
+    // every member steps (no branch around the physics); the near-zero sin/cos vote counts
+    // the live members alone, since a terminated member's results are discarded
+    const bool done = advance(x, xd, th, thd, (l1 > l0) ? 1 : 0, alive);
     if (alive) {
-      if (advance(x, xd, th, thd, (l1 > l0) ? 1 : 0)) {
+      if (done) {
         alive = false;
       } else {
         survived += 1.0f;

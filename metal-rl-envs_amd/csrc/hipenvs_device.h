@@ -118,8 +118,10 @@ __device__ __forceinline__ void det_sincos(float x, float* sin_out, float* cos_o
 // active lane of the wave has |x| <= 0.78, rint(x * 2/pi) is 0 on every lane, the reduction
 // returns x itself (a zero of either sign gives the same sin and cos), and the quadrant is
 // 0, so the polynomial alone returns det_sincos's bits. Otherwise the wave takes det_sincos.
-__device__ __forceinline__ void det_sincos_near_zero(float x, float* sin_out, float* cos_out) {
-  if (__all(fabsf(x) <= 0.78f)) {
+// Lanes with `counts` false take no part in the vote, and their results are not det_sincos's
+// when the wave takes the polynomial: for callers that discard those lanes' results.
+__device__ __forceinline__ void det_sincos_near_zero(float x, float* sin_out, float* cos_out, bool counts = true) {
+  if (__all(!counts || fabsf(x) <= 0.78f)) {
     sincos_poly(x, sin_out, cos_out);
   } else {
     det_sincos(x, sin_out, cos_out);
