@@ -117,7 +117,10 @@ __device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double 
 // (v_free + M^-1 J_t^T lt) + M^-1 J_n^T ln (hopper_np.py:76), instead of the legged body's
 // v_free + (M^-1 J_t^T lt + M^-1 J_n^T ln) (legged_np.py:95); otherwise the hopper is this
 // body at C = 1 with one sweep.
-template <int C, class Div, int kGroup = 0, bool kHopperSum = false>
+// kStage (one-lane form only) parks the M^-1 J^T columns in LDS during the Gauss-Seidel
+// sweeps, at xs[e * 64] for element e (xs points at the lane's own column of a 64-lane
+// block), which frees 2C(3 + C) registers there; they are read back for the velocity update.
+template <int C, class Div, int kGroup = 0, bool kHopperSum = false, bool kStage = false>
 __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
                                         float assist, float assist_damping, Div& div, float* xs = nullptr,
                                         int g = 0) {
@@ -259,6 +262,18 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     w0t[k] = (vf[0] + ca[k] * vf[2]) + ca[k] * vf[3 + k];
     w0n[k] = (vf[1] + sa[k] * vf[2]) + sa[k] * vf[3 + k];
   }
+  if constexpr (kStage) {
+    static_assert(kGroup == 0, "staging is for the one-lane form");
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        xs[(k * N + i) * 64] = MiJt[k][i];
+        xs[((C + k) * N + i) * 64] = MiJn[k][i];
+      }
+    }
+    asm volatile("" ::: "memory");  // the columns live in LDS until the velocity update
+  }
   // block projected Gauss-Seidel, fixed contact order (legged_np.py:88-93)
   float lt[C], ln[C];
   ContactBlock blk[C];
@@ -288,6 +303,17 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     }
   }
   // v = v_free + sum_k M^-1 J_k^T lambda_k; q += h v
+  if constexpr (kStage) {
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        MiJt[k][i] = xs[(k * N + i) * 64];
+        MiJn[k][i] = xs[((C + k) * N + i) * 64];
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     float vn;
@@ -308,9 +334,9 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
 // One substep dividing through the shared float64 reciprocals; a lane on which a quotient
 // came out subnormal (never met in practice) redoes the substep from its saved state with
 // IEEE division, so the result is always the IEEE one.
-template <int C, bool kHopperSum = false>
+template <int C, bool kHopperSum = false, bool kStage = false>
 __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
-                                              float assist, float assist_damping) {
+                                              float assist, float assist_damping, float* stage = nullptr) {
   constexpr int N = 3 + C;
   float q0[N], v0[N];
 #pragma unroll
@@ -319,7 +345,7 @@ __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + 
     v0[i] = v[i];
   }
   DivRecip fast;
-  substep<C, DivRecip, 0, kHopperSum>(q, v, tq, iters, assist, assist_damping, fast);
+  substep<C, DivRecip, 0, kHopperSum, kStage>(q, v, tq, iters, assist, assist_damping, fast, stage);
   if (fast.saw_subnormal()) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
@@ -327,7 +353,7 @@ __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + 
       v[i] = v0[i];
     }
     DivIEEE ieee;
-    substep<C, DivIEEE, 0, kHopperSum>(q, v, tq, iters, assist, assist_damping, ieee);
+    substep<C, DivIEEE, 0, kHopperSum, kStage>(q, v, tq, iters, assist, assist_damping, ieee, stage);
   }
 }
 
@@ -368,10 +394,18 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
 #define LEGGED_ROLLOUT_MIN_WAVES 1
 #endif
 // The same for the first chunk of the compacting schedule, which streams every member's
-// weights from HBM. Two waves per SIMD there (256 registers, 32 spilled) made the whole
-// rollout slower (64.4 -> 94.3 ms at the ES benchmark's shape), so one wave keeps them all.
+// weights from HBM.
 #ifndef LEGGED_FIRST_CHUNK_MIN_WAVES
 #define LEGGED_FIRST_CHUNK_MIN_WAVES 1
+#endif
+// Whether the chunk kernels park the substep's M^-1 J^T columns in LDS during the
+// Gauss-Seidel sweeps (substep's kStage, 14 KB per single-wave workgroup at C = 4). The
+// sweeps hold the most registers; with the columns in LDS the C = 4 chunk kernels need about
+// 210 instead of 263-271, so two waves share a SIMD and one streams weights while the other
+// runs the physics (ES rollout at N = 262,144: 64.2 -> 61.3 ms at 8 sweeps, 89.2 -> 83.7 ms
+// at 16). Forcing two waves without it spilled to scratch and ran slower (94 ms at 8).
+#ifndef LEGGED_CHUNK_STAGE
+#define LEGGED_CHUNK_STAGE 1
 #endif
 
 // POLICY_UNROLL hidden units per policy loop iteration bounds how many of the member's
@@ -754,6 +788,8 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
                                                            float* __restrict__ steps_out, int64_t wide_max) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  constexpr bool kStage = LEGGED_CHUNK_STAGE != 0;
+  __shared__ float stage_lds[kStage ? 2 * C * N * 64 : 1];
   const unsigned lane = threadIdx.x;
   const int64_t count = kFirst ? p : (int64_t)*src.count;
   if (!kFirst && count <= wide_max) return;  // rollout_tail_kernel takes the set (the same count everywhere)
@@ -792,7 +828,8 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
         policy_torques<C, HID, UnitRows, kTile>(w, kTile, q, v, tq);
       }
 #pragma unroll 1
-      for (int sub = 0; sub < SUBSTEPS; ++sub) substep_exact<C>(q, v, tq, iters, assist, assist_damping);
+      for (int sub = 0; sub < SUBSTEPS; ++sub)
+        substep_exact<C, false, kStage>(q, v, tq, iters, assist, assist_damping, stage_lds + lane);
       ++t;
       bool finished;
       if (fallen<C>(q)) {
