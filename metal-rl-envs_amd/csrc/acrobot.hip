@@ -171,11 +171,6 @@ constexpr int kRolloutMembers = 64 / kRolloutLanes;
 // three) and every lane of the 16-lane group (one DPP row) receives the results by row
 // broadcast. Each value is the single-lane function's on the same argument, so the bits
 // are those of dsdt/rk4/terminal.
-template <int L>
-__device__ __forceinline__ float group_bcast(float v) {  // DPP row_newbcast:L
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
-}
-
 struct GroupTrig {
   float sin_a, cos_a, sin_b, cos_b, cos_ab;  // theta1, theta2, theta2 + theta1
 };

@@ -105,11 +105,22 @@ __device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double 
   }
 }
 
+// sa[k], ca[k] = lane k's sn, cs, for k < K, on every lane of the 16-lane row.
+template <int K>
+__device__ __forceinline__ void row_trig(float sn, float cs, float* sa, float* ca) {
+  if constexpr (K > 0) {
+    row_trig<K - 1>(sn, cs, sa, ca);
+    sa[K - 1] = group_bcast<K - 1>(sn);
+    ca[K - 1] = group_bcast<K - 1>(cs);
+  }
+}
+
 // One semi-implicit Euler substep with block PGS contacts, in place (legged_np.py:57-97).
 // kGroup = 0: one lane computes the whole substep. kGroup = G > 0: the G lanes g = 0..G-1 of
-// a member's group all hold the member's state and compute everything identically, except
-// the 2C + 1 triangular solves: lane g < 2C + 1 solves right-hand side g (the forces, then
-// the tangent, then the normal Jacobian rows) and the results are exchanged through the
+// a member's group (one 16-lane DPP row) all hold the member's state and compute everything
+// identically, except that lane g < C evaluates foot g's sin and cos, shared by row
+// broadcast, and lane g < 2C + 1 solves right-hand side g of the 2C + 1 triangular solves
+// (the forces, then the tangent, then the normal Jacobian rows), exchanged through the
 // group's LDS rows xs ((2C + 1) x 8 floats). Every value is computed by the same expression
 // as in the one-lane form, so the results are the same bits. Callers keep the group's
 // lanes in one single-wave workgroup, so the barriers order its LDS traffic.
@@ -123,13 +134,24 @@ __device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double 
 template <int C, class Div, int kGroup = 0, bool kHopperSum = false, bool kStage = false>
 __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C], int iters,
                                         float assist, float assist_damping, Div& div, float* xs = nullptr,
-                                        int g = 0) {
+                                        int g = 0, float* xd = nullptr) {
   constexpr int N = 3 + C;
   float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
+  if constexpr (kGroup > 0) {
+    // lane g < C evaluates foot g's sin and cos; the group's 16 lanes are one DPP row
+    static_assert(kGroup == 16 && C <= 16, "the group is one 16-lane DPP row");
+    float a = q[2] + q[3];
+#pragma unroll
+    for (int k = 1; k < C; ++k) a = (g == k) ? q[2] + q[3 + k] : a;
+    float sn, cs;
+    det_sincos(a, &sn, &cs);
+    row_trig<C>(sn, cs, sa, ca);
+  } else {
+#pragma unroll
+    for (int k = 0; k < C; ++k) det_sincos(q[2] + q[3 + k], &sa[k], &ca[k]);
+  }
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const float a = q[2] + q[3 + k];
-    det_sincos(a, &sa[k], &ca[k]);
     const float ad = v[2] + v[3 + k];
     dx[k] = ((-sa[k]) * ad) * ad;
     dy[k] = (ca[k] * ad) * ad;
@@ -250,15 +272,59 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
   for (int i = 0; i < N; ++i) vf[i] = v[i] + H * f[i];
   // Delassus blocks A[k][l] = (Jt_k.MiJt_l, Jt_k.MiJn_l, Jn_k.MiJt_l, Jn_k.MiJn_l) and free velocities
   float Att[C][C], Atn[C][C], Ant[C][C], Ann[C][C], w0t[C], w0n[C];
+  if constexpr (kGroup > 0) {
+    // lane g < C^2 forms block (g / C, g % C) from the solved rows in xs, and a lane of a
+    // diagonal block also forms its contact's ContactBlock; the group reads the C^2 blocks
+    // (4 floats each) and the C contact blocks (12 floats each) back from xd
+    static_assert(C * C <= kGroup, "one lane per block");
+    constexpr int kRow = 8;
+    const int gb = g < C * C ? g : 0;  // lanes past C^2 form block 0 again, unused
+    const int kb = gb / C, lb = gb % C;
+    float ck = ca[0], sk = sa[0];
+#pragma unroll
+    for (int kk = 1; kk < C; ++kk) {
+      ck = (kb == kk) ? ca[kk] : ck;
+      sk = (kb == kk) ? sa[kk] : sk;
+    }
+    const float* rt = xs + (1 + lb) * kRow;
+    const float* rn = xs + (1 + C + lb) * kRow;
+    const float t2 = rt[2], t3 = rt[3 + kb], n2 = rn[2], n3 = rn[3 + kb];
+    const float4 blk4 = make_float4((rt[0] + ck * t2) + ck * t3, (rn[0] + ck * n2) + ck * n3,
+                                    (rt[1] + sk * t2) + sk * t3, (rn[1] + sk * n2) + sk * n3);
+    if (g < C * C) *reinterpret_cast<float4*>(xd + 4 * g) = blk4;
+    const ContactBlock own = contact_block(blk4.x, blk4.y, blk4.w);
+    if (g < C * C && kb == lb) {
+      float* xc = xd + 4 * C * C + 12 * kb;
+      *reinterpret_cast<float4*>(xc) = make_float4(own.det, own.den_p, own.den_m, 0.0f);
+      *reinterpret_cast<double2*>(xc + 4) = make_double2(own.rdet, own.rden_p);
+      *reinterpret_cast<double*>(xc + 8) = own.rden_m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+#pragma unroll
+      for (int l = 0; l < C; ++l) {
+        const float4 e = *reinterpret_cast<const float4*>(xd + 4 * (k * C + l));
+        Att[k][l] = e.x;
+        Atn[k][l] = e.y;
+        Ant[k][l] = e.z;
+        Ann[k][l] = e.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+#pragma unroll
+      for (int l = 0; l < C; ++l) {
+        Att[k][l] = (MiJt[l][0] + ca[k] * MiJt[l][2]) + ca[k] * MiJt[l][3 + k];
+        Atn[k][l] = (MiJn[l][0] + ca[k] * MiJn[l][2]) + ca[k] * MiJn[l][3 + k];
+        Ant[k][l] = (MiJt[l][1] + sa[k] * MiJt[l][2]) + sa[k] * MiJt[l][3 + k];
+        Ann[k][l] = (MiJn[l][1] + sa[k] * MiJn[l][2]) + sa[k] * MiJn[l][3 + k];
+      }
+    }
+  }
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-#pragma unroll
-    for (int l = 0; l < C; ++l) {
-      Att[k][l] = (MiJt[l][0] + ca[k] * MiJt[l][2]) + ca[k] * MiJt[l][3 + k];
-      Atn[k][l] = (MiJn[l][0] + ca[k] * MiJn[l][2]) + ca[k] * MiJn[l][3 + k];
-      Ant[k][l] = (MiJt[l][1] + sa[k] * MiJt[l][2]) + sa[k] * MiJt[l][3 + k];
-      Ann[k][l] = (MiJn[l][1] + sa[k] * MiJn[l][2]) + sa[k] * MiJn[l][3 + k];
-    }
     w0t[k] = (vf[0] + ca[k] * vf[2]) + ca[k] * vf[3 + k];
     w0n[k] = (vf[1] + sa[k] * vf[2]) + sa[k] * vf[3 + k];
   }
@@ -281,7 +347,15 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
   for (int k = 0; k < C; ++k) {
     lt[k] = 0.0f;
     ln[k] = 0.0f;
-    blk[k] = contact_block(Att[k][k], Atn[k][k], Ann[k][k]);
+    if constexpr (kGroup > 0) {
+      const float* xc = xd + 4 * C * C + 12 * k;
+      const float4 f4 = *reinterpret_cast<const float4*>(xc);
+      const double2 d2 = *reinterpret_cast<const double2*>(xc + 4);
+      blk[k] = ContactBlock{Att[k][k], Atn[k][k], Ann[k][k], f4.x, f4.y, f4.z,
+                            d2.x, d2.y, *reinterpret_cast<const double*>(xc + 8)};
+    } else {
+      blk[k] = contact_block(Att[k][k], Atn[k][k], Ann[k][k]);
+    }
   }
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
@@ -363,7 +437,7 @@ __device__ __forceinline__ void substep_exact(float (&q)[3 + C], float (&v)[3 + 
 template <int C, int G>
 __device__ __forceinline__ void substep_exact_group(float (&q)[3 + C], float (&v)[3 + C], const float (&tq)[C],
                                                     int iters, float assist, float assist_damping, float* xs, int g,
-                                                    bool live) {
+                                                    bool live, float* xd) {
   constexpr int N = 3 + C;
   float q0[N], v0[N];
 #pragma unroll
@@ -372,7 +446,7 @@ __device__ __forceinline__ void substep_exact_group(float (&q)[3 + C], float (&v
     v0[i] = v[i];
   }
   DivRecip fast;
-  substep<C, DivRecip, G>(q, v, tq, iters, assist, assist_damping, fast, xs, g);
+  substep<C, DivRecip, G>(q, v, tq, iters, assist, assist_damping, fast, xs, g, xd);
   if (__any(live && fast.saw_subnormal())) {  // lanes of finished members step on, unused
 #pragma unroll
     for (int i = 0; i < N; ++i) {
@@ -380,7 +454,7 @@ __device__ __forceinline__ void substep_exact_group(float (&q)[3 + C], float (&v
       v[i] = v0[i];
     }
     DivIEEE ieee;
-    substep<C, DivIEEE, G>(q, v, tq, iters, assist, assist_damping, ieee, xs, g);
+    substep<C, DivIEEE, G>(q, v, tq, iters, assist, assist_damping, ieee, xs, g, xd);
   }
 }
 
@@ -704,18 +778,22 @@ constexpr int kGroupLanes = 16;
 #define LEGGED_TAIL_MEMBERS_PER_CU 16  // survivors per CU at the switch: one 4-member wave per SIMD
 #endif
 constexpr int kGroupMembers = 64 / kGroupLanes;
+// LDS floats per member for the group substep's Delassus and contact blocks (xd)
+template <int C>
+constexpr int kBlockFloats = 4 * C * C + 12 * C;
 
 template <int C, int HID>
 __device__ __forceinline__ void rollout_group_tail(const Packed& src, int64_t count, int64_t cap, int32_t horizon,
                                                    int iters, float alive_bonus, float fall, float gate,
                                                    float assist, float assist_damping, float* __restrict__ fitness,
                                                    float* __restrict__ steps_out, float* xs_all, float* xh_all,
-                                                   float* xl_all) {
+                                                   float* xl_all, float* xd_all) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
   constexpr int G = kGroupLanes, M = kGroupMembers;
   const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
   float* xs = xs_all + mloc * (2 * C + 1) * 8;
+  float* xd = xd_all + mloc * kBlockFloats<C>;
   float* xh = xh_all + mloc * HID;
   float* xl = xl_all + mloc * 16;
   for (int64_t mbase = (int64_t)blockIdx.x * M; mbase < count; mbase += (int64_t)gridDim.x * M) {
@@ -736,7 +814,7 @@ __device__ __forceinline__ void rollout_group_tail(const Packed& src, int64_t co
       policy_group<C, HID, G>(w, q, v, tq, xh, xl, g);
 #pragma unroll 1
       for (int sub = 0; sub < SUBSTEPS; ++sub)
-        substep_exact_group<C, G>(q, v, tq, iters, assist, assist_damping, xs, g, live);
+        substep_exact_group<C, G>(q, v, tq, iters, assist, assist_damping, xs, g, live, xd);
       if (live) {
         ++t;
         bool finished;
@@ -772,10 +850,11 @@ __global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t ca
   const int64_t count = (int64_t)*src.count;
   if (count > wide_max) return;
   __shared__ float xs_all[kGroupMembers * (2 * C + 1) * 8];
+  __shared__ __align__(16) float xd_all[kGroupMembers * kBlockFloats<C>];
   __shared__ float xh_all[kGroupMembers * HID];
   __shared__ float xl_all[kGroupMembers * 16];
   rollout_group_tail<C, HID>(src, count, cap, horizon, iters, alive_bonus, fall, gate, assist, assist_damping, fitness,
-                             steps_out, xs_all, xh_all, xl_all);
+                             steps_out, xs_all, xh_all, xl_all, xd_all);
 }
 
 template <int C, int HID, bool kFirst>
