@@ -258,14 +258,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < N; ++i) f[i] = xs[i];
-#pragma unroll
-    for (int kk = 0; kk < C; ++kk) {
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        MiJt[kk][i] = xs[(1 + kk) * kRow + i];
-        MiJn[kk][i] = xs[(1 + C + kk) * kRow + i];
-      }
-    }
+    // the M^-1 J^T columns stay in xs until the velocity update reads them
   }
   float vf[N];
 #pragma unroll
@@ -385,6 +378,17 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       for (int i = 0; i < N; ++i) {
         MiJt[k][i] = xs[(k * N + i) * 64];
         MiJn[k][i] = xs[((C + k) * N + i) * 64];
+      }
+    }
+  } else if constexpr (kGroup > 0) {
+    constexpr int kRow = 8;
+    asm volatile("" ::: "memory");  // read here, not held in registers through the sweeps
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        MiJt[k][i] = xs[(1 + k) * kRow + i];
+        MiJn[k][i] = xs[(1 + C + k) * kRow + i];
       }
     }
   }
@@ -777,17 +781,25 @@ constexpr int kGroupLanes = 16;
 #ifndef LEGGED_TAIL_MEMBERS_PER_CU
 #define LEGGED_TAIL_MEMBERS_PER_CU 16  // survivors per CU at the switch: one 4-member wave per SIMD
 #endif
+// Above the tail's bound and up to this many survivors per CU, a chunk runs in the group form
+// (rollout_group_chunk_kernel) instead of one member per lane.
+#ifndef LEGGED_GROUP_CHUNK_MEMBERS_PER_CU
+#define LEGGED_GROUP_CHUNK_MEMBERS_PER_CU 32
+#endif
 constexpr int kGroupMembers = 64 / kGroupLanes;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
 template <int C>
 constexpr int kBlockFloats = 4 * C * C + 12 * C;
 
-template <int C, int HID>
-__device__ __forceinline__ void rollout_group_tail(const Packed& src, int64_t count, int64_t cap, int32_t horizon,
-                                                   int iters, float alive_bonus, float fall, float gate,
-                                                   float assist, float assist_damping, float* __restrict__ fitness,
-                                                   float* __restrict__ steps_out, float* xs_all, float* xh_all,
-                                                   float* xl_all, float* xd_all) {
+// kChunk false: every member runs to the end of its episode. kChunk true: at most chunk_steps
+// steps, then the survivors are appended to dst like rollout_chunk_kernel's (the member's
+// group copies its weight rows).
+template <int C, int HID, bool kChunk>
+__device__ __forceinline__ void rollout_group(const Packed& src, const Packed& dst, int64_t count, int64_t cap,
+                                              int32_t chunk_steps, int32_t horizon, int iters, float alive_bonus,
+                                              float fall, float gate, float assist, float assist_damping,
+                                              float* __restrict__ fitness, float* __restrict__ steps_out,
+                                              float* xs_all, float* xh_all, float* xl_all, float* xd_all) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
   constexpr int G = kGroupLanes, M = kGroupMembers;
@@ -810,7 +822,8 @@ __device__ __forceinline__ void rollout_group_tail(const Packed& src, int64_t co
     const int32_t id = src.meta[slot];
     int32_t t = src.meta[cap + slot];
     const float* w = src.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
-    while (__any(live)) {  // every lane steps, so the groups' barriers stay uniform
+    // every lane steps while any member of the wave is live, so the barriers stay uniform
+    for (int32_t k = 0; (!kChunk || k < chunk_steps) && __any(live); ++k) {
       policy_group<C, HID, G>(w, q, v, tq, xh, xl, g);
 #pragma unroll 1
       for (int sub = 0; sub < SUBSTEPS; ++sub)
@@ -836,12 +849,46 @@ __device__ __forceinline__ void rollout_group_tail(const Packed& src, int64_t co
         }
       }
     }
+    if constexpr (kChunk) {
+      // one slot per surviving member (its lane 0 counts), in lane order
+      const unsigned long long m = __ballot(live && g == 0);
+      if (m) {
+        const int leader = __ffsll((long long)m) - 1;
+        unsigned int slot0 = 0;
+        if ((int)threadIdx.x == leader) slot0 = atomicAdd(dst.count, (unsigned int)__popcll(m));
+        slot0 = __shfl(slot0, leader);
+        if (live) {
+          const int64_t to = (int64_t)slot0 + __popcll(m & ((1ull << (mloc * G)) - 1ull));
+          if (g == 0) {
+#pragma unroll
+            for (int r = 0; r < N; ++r) {
+              dst.state[r * cap + to] = q[r];
+              dst.state[(N + r) * cap + to] = v[r];
+            }
+            dst.acc[to] = total;
+            dst.acc[cap + to] = taken;
+            dst.meta[to] = id;
+            dst.meta[cap + to] = t;
+          }
+          float* wd = dst.theta + (to / kTile) * (int64_t)D * kTile + (to % kTile);
+          for (int d = g; d < D; d += G) wd[d * kTile] = w[d * kTile];
+        }
+      }
+    }
   }
 }
 
+// LDS of the group kernels: per member, the solve rows, the Delassus and contact blocks, the
+// hidden values and the head values.
+#define LEGGED_GROUP_LDS(C, HID)                                                   \
+  __shared__ float xs_all[kGroupMembers * (2 * (C) + 1) * 8];                      \
+  __shared__ __align__(16) float xd_all[kGroupMembers * kBlockFloats<(C)>];        \
+  __shared__ float xh_all[kGroupMembers * (HID)];                                  \
+  __shared__ float xl_all[kGroupMembers * 16]
+
 // The group tail as a kernel of its own, launched after every later chunk: it runs when the
-// set holds at most wide_max members and exits at once otherwise (rollout_chunk_kernel does
-// the opposite). Kept apart so that the one-lane kernel's code is compiled on its own.
+// set holds at most wide_max members and exits at once otherwise (the chunk kernels do the
+// opposite). Kept apart so that the one-lane kernel's code is compiled on its own.
 template <int C, int HID>
 __global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t cap, int32_t horizon, int iters,
                                                           float alive_bonus, float fall, float gate, float assist,
@@ -849,12 +896,26 @@ __global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t ca
                                                           float* __restrict__ steps_out, int64_t wide_max) {
   const int64_t count = (int64_t)*src.count;
   if (count > wide_max) return;
-  __shared__ float xs_all[kGroupMembers * (2 * C + 1) * 8];
-  __shared__ __align__(16) float xd_all[kGroupMembers * kBlockFloats<C>];
-  __shared__ float xh_all[kGroupMembers * HID];
-  __shared__ float xl_all[kGroupMembers * 16];
-  rollout_group_tail<C, HID>(src, count, cap, horizon, iters, alive_bonus, fall, gate, assist, assist_damping, fitness,
-                             steps_out, xs_all, xh_all, xl_all, xd_all);
+  LEGGED_GROUP_LDS(C, HID);
+  rollout_group<C, HID, false>(src, src, count, cap, horizon, horizon, iters, alive_bonus, fall, gate, assist,
+                               assist_damping, fitness, steps_out, xs_all, xh_all, xl_all, xd_all);
+}
+
+// The group form for one chunk, when the set holds more than lo and at most hi members
+// (a few waves of four members per SIMD): the survivors go to dst as after a one-lane chunk.
+template <int C, int HID>
+__global__ __launch_bounds__(64, 2) void rollout_group_chunk_kernel(Packed src, Packed dst, int64_t cap,
+                                                                    int32_t chunk_steps, int32_t horizon, int iters,
+                                                                    float alive_bonus, float fall, float gate,
+                                                                    float assist, float assist_damping,
+                                                                    float* __restrict__ fitness,
+                                                                    float* __restrict__ steps_out, int64_t lo,
+                                                                    int64_t hi) {
+  const int64_t count = (int64_t)*src.count;
+  if (count <= lo || count > hi) return;
+  LEGGED_GROUP_LDS(C, HID);
+  rollout_group<C, HID, true>(src, dst, count, cap, chunk_steps, horizon, iters, alive_bonus, fall, gate, assist,
+                              assist_damping, fitness, steps_out, xs_all, xh_all, xl_all, xd_all);
 }
 
 template <int C, int HID, bool kFirst>
@@ -864,14 +925,14 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
                                                            int32_t chunk_steps, int32_t horizon, int iters,
                                                            float alive_bonus, float fall, float gate, float assist,
                                                            float assist_damping, float* __restrict__ fitness,
-                                                           float* __restrict__ steps_out, int64_t wide_max) {
+                                                           float* __restrict__ steps_out, int64_t group_max) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
   constexpr bool kStage = LEGGED_CHUNK_STAGE != 0;
   __shared__ float stage_lds[kStage ? 2 * C * N * 64 : 1];
   const unsigned lane = threadIdx.x;
   const int64_t count = kFirst ? p : (int64_t)*src.count;
-  if (!kFirst && count <= wide_max) return;  // rollout_tail_kernel takes the set (the same count everywhere)
+  if (!kFirst && count <= group_max) return;  // a group kernel takes the set (the same count everywhere)
   const int64_t src_stride = kFirst ? p : cap;  // state rows; the weights use tiles after the first chunk
   const float* sstate = kFirst ? state0 : src.state;
   const float* stheta = kFirst ? theta0 : src.theta;
@@ -1031,6 +1092,45 @@ __global__ __launch_bounds__(64) void seed_set_kernel(const float* __restrict__ 
   }
 }
 
+// Member counts at which the schedule changes form: one member per lane above group_max,
+// the group chunk kernel above wide_max, the group tail at or below wide_max.
+struct GroupBounds {
+  int64_t wide_max, group_max, group_grid, tail_grid;
+};
+
+inline GroupBounds group_bounds(int64_t p, int cus) {
+  GroupBounds b;
+  b.wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * cus;
+  const int64_t gm = (int64_t)LEGGED_GROUP_CHUNK_MEMBERS_PER_CU * cus;
+  b.group_max = gm > b.wide_max ? gm : b.wide_max;
+  // one member group per workgroup: a kernel never holds more than min(p, its bound) members
+  const int64_t group_members = p < b.group_max ? p : b.group_max;
+  const int64_t tail_members = p < b.wide_max ? p : b.wide_max;
+  b.group_grid = (group_members + kGroupMembers - 1) / kGroupMembers;
+  b.tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
+  return b;
+}
+
+// One later chunk from set src into set dst: of the three kernels, the one whose member
+// bound holds src's count runs, the others exit at once.
+template <int C, int HID>
+int launch_later_chunk(const float* state0, const float* theta0, int64_t p, const Packed& src, const Packed& dst,
+                       int64_t cap, int64_t grid, const GroupBounds& gb, int32_t chunk_steps, int32_t horizon,
+                       int iters, float alive, float fall, float gate, float af, float ad, float* fitness,
+                       float* steps, hipStream_t s) {
+  hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, dst.count, 0u);
+  hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state0, theta0, p,
+                     src, dst, cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
+                     gb.group_max);
+  if (gb.group_max > gb.wide_max)
+    hipLaunchKernelGGL((rollout_group_chunk_kernel<C, HID>), dim3((unsigned)gb.group_grid), dim3(64), 0, s, src, dst,
+                       cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps, gb.wide_max,
+                       gb.group_max);
+  hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)gb.tail_grid), dim3(64), 0, s, src, cap, horizon,
+                     iters, alive, fall, gate, af, ad, fitness, steps, gb.wide_max);
+  return launch_status();
+}
+
 template <int C, int HID>
 int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32_t horizon, int iters,
                    int32_t chunk_steps, float alive, float fall, float gate, double assist, float* fitness,
@@ -1064,27 +1164,17 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   const float af = (float)assist, ad = (float)(0.1 * assist);
   // first chunk: the caller's arrays -> set 0
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
-  // the group tail takes over once the survivors fit kGroupMembers to a wave at one wave per SIMD
-  const int64_t wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * cus;
+  const GroupBounds gb = group_bounds(p, cus);
   hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true>), dim3((unsigned)needed), dim3(64), 0, s, state, theta_cols,
                      p, set[1], set[0], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
-                     wide_max);
+                     gb.group_max);
   int status = launch_status();
   int cur = 0;
   const int64_t grid = resident < needed ? resident : needed;
-  // one member group per workgroup: the tail never holds more than min(p, wide_max) members
-  const int64_t tail_members = p < wide_max ? p : wide_max;
-  const int64_t tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
   for (int64_t done = chunk_steps; status == HIPENVS_OK && done < horizon; done += chunk_steps) {
-    const int nxt = 1 - cur;
-    hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[nxt].count, 0u);
-    hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state, theta_cols,
-                       p, set[cur], set[nxt], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness,
-                       steps, wide_max);
-    hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)tail_grid), dim3(64), 0, s, set[cur], cap,
-                       horizon, iters, alive, fall, gate, af, ad, fitness, steps, wide_max);
-    status = launch_status();
-    cur = nxt;
+    status = launch_later_chunk<C, HID>(state, theta_cols, p, set[cur], set[1 - cur], cap, grid, gb, chunk_steps,
+                                        horizon, iters, alive, fall, gate, af, ad, fitness, steps, s);
+    cur = 1 - cur;
   }
   return status;
 }
@@ -1122,9 +1212,7 @@ int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uin
   const int64_t needed = (p + 63) / 64;
   const int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
   const int64_t grid = resident < needed ? resident : needed;
-  const int64_t wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * cus;
-  const int64_t tail_members = p < wide_max ? p : wide_max;
-  const int64_t tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
+  const GroupBounds gb = group_bounds(p, cus);
   const float af = (float)assist, ad = (float)(0.1 * assist);
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, (uint32_t)p);
   hipLaunchKernelGGL((seed_set_kernel<C, HID>), dim3((unsigned)((p / 2 + 63) / 64)), dim3(64), 0, s, state, theta, p,
@@ -1132,15 +1220,9 @@ int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uin
   int status = launch_status();
   int cur = 0;
   for (int64_t done = 0; status == HIPENVS_OK && done < horizon; done += chunk_steps) {
-    const int nxt = 1 - cur;
-    hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[nxt].count, 0u);
-    hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state, theta, p,
-                       set[cur], set[nxt], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness,
-                       steps, wide_max);
-    hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)tail_grid), dim3(64), 0, s, set[cur], cap,
-                       horizon, iters, alive, fall, gate, af, ad, fitness, steps, wide_max);
-    status = launch_status();
-    cur = nxt;
+    status = launch_later_chunk<C, HID>(state, theta, p, set[cur], set[1 - cur], cap, grid, gb, chunk_steps, horizon,
+                                        iters, alive, fall, gate, af, ad, fitness, steps, s);
+    cur = 1 - cur;
   }
   return status;
 }

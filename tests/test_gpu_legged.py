@@ -137,6 +137,28 @@ def test_group_tail_equals_static(dev, c, hidden):
         assert ss.max().item() > 8  # members outlived the first chunk
 
 
+@pytest.mark.parametrize("c,hidden", [(1, 4), (2, 32), (4, 64)])
+def test_group_chunk_equals_static(dev, c, hidden):
+    """Populations of 24 members per CU: above the group tail's bound (16 per CU) and within
+    the group chunk's (32 per CU), so later chunks run in the group form and append their
+    survivors (every chunk, with the assist keeping all members up; until the count falls
+    to the tail's bound, without it): member for member equal to the one-lane kernel."""
+    from hipenvs import legged, legged_rollout
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    p, horizon = 24 * cus, 60
+    state = legged.Legged(c).reset(p, seed=6, device=dev)
+    past_first = 0
+    for assist, scale in ((0.0, 0.3), (20.0, 0.0)):
+        theta = torch.from_numpy(_population(p, c, hidden, scale, 7 * c + hidden)).to(dev)
+        fq, sq = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="chunked",
+                                        chunk_steps=8)
+        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="rows")
+        assert torch.equal(fq, fs) and torch.equal(sq, ss), (c, hidden, assist)
+        past_first = max(past_first, int((ss > 8).sum().item()))
+    assert past_first > 16 * cus  # the second chunk ran in the group form
+
+
 def test_shaped_reward_and_assist_match_oracle(dev):
     """test_es.py:71-104's variants: alive 0.1 + fall penalty 20 (some fitness negative),
     and the assist spring with a gate."""
