@@ -72,8 +72,12 @@ __device__ __forceinline__ void contact_impulse(const ContactBlock& b, float wt,
   const float ln_stick = div(Att * tw + Atn * wt, b.det, b.rdet);
   const float lt_stick = div((-Ann) * wt - Atn * tw, b.det, b.rdet);
   const bool sticks = fabsf(lt_stick) <= MU * ln_stick;
-  const float ln_p = (b.den_p > 0.0f) ? max0(div(tw, b.den_p, b.rden_p)) : 0.0f;
-  const float ln_m = (b.den_m > 0.0f) ? max0(div(tw, b.den_m, b.rden_m)) : 0.0f;
+  // both cone quotients are formed whatever the signs of their denominators and selected
+  // after (no branch); a subnormal mark from an unused one only costs an exact redo
+  const float q_p = div(tw, b.den_p, b.rden_p);
+  const float q_m = div(tw, b.den_m, b.rden_m);
+  const float ln_p = (b.den_p > 0.0f) ? max0(q_p) : 0.0f;
+  const float ln_m = (b.den_m > 0.0f) ? max0(q_m) : 0.0f;
   const float slip_p = wt + (Att * MU + Atn) * ln_p;
   const float s = (slip_p <= 0.0f) ? 1.0f : -1.0f;
   const float ln_slide = (slip_p <= 0.0f) ? ln_p : ln_m;
