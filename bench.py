@@ -350,8 +350,9 @@ def legged_population(dev, p, c, hidden, sigma=0.03, seed=0):
     return theta0[None, :] + sigma * torch.cat([half, -half], dim=0)
 
 
-def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats):
-    """(median wall s, median HIP-event s, steps taken, mean fitness) of full rollouts."""
+def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats, alive_at=()):
+    """(median wall s, median HIP-event s, steps taken, mean fitness) of full rollouts, and
+    with alive_at the members still alive after each of those step counts."""
     import torch
 
     from hipenvs import legged_rollout
@@ -376,7 +377,16 @@ def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats):
         walls.append(time.perf_counter() - t0)
         evs.append(start.elapsed_time(end) / 1e3)
         taken = float(steps.double().sum().item())
-    return statistics.median(walls), statistics.median(evs), taken, float(fit.mean().item())
+    out = (statistics.median(walls), statistics.median(evs), taken, float(fit.mean().item()))
+    if alive_at:
+        alive = {t: int((steps > t).sum().item()) for t in alive_at}
+        alive["steps_in_first_32"] = int(torch.clamp(steps, max=32).double().sum().item())
+        return out + (alive,)
+    return out
+
+
+# step counts at which the legged benchmark reports how many members are still alive
+ALIVE_AT = (32, 64, 96, 128, 160, 192, 224, 256, 512, 999)
 
 
 def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
@@ -390,7 +400,8 @@ def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
     out = {"n_envs": p, "c": c, "hidden": hidden, "horizon": horizon, "sigma": 0.03, "alive_bonus": 1.0,
            "schedule": f"chunked ({legged_rollout.CHUNK_STEPS} steps), columns layout", "by_sweeps": {}}
     for s in sweeps_list:
-        wall, ev, taken, fit_mean = time_rollout(state, theta_cols, hidden, horizon, c, s, "chunked", args.repeats)
+        wall, ev, taken, fit_mean, alive = time_rollout(state, theta_cols, hidden, horizon, c, s, "chunked",
+                                                        args.repeats, alive_at=ALIVE_AT)
         flops = legged_flops_per_step(c, s, hidden)
         achieved_tf = taken * flops / ev / 1e12
         rec = {
@@ -406,11 +417,14 @@ def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
             "weight_bytes_per_env_step": 4 * d,
             "weight_stream_gbs": taken * 4 * d / ev / 1e9,
             "fitness_mean": fit_mean,
+            "alive_after_steps": {str(t): n for t, n in alive.items()},
         }
         out["by_sweeps"][str(s)] = rec
         log(f"legged4 ES rollout N={p} H={hidden} S={s} (chunked): {rec['env_steps_per_s']:,.0f} env-steps/s "
             f"(mean episode {taken / p:.1f} steps, {ev * 1e3:.1f} ms), {achieved_tf:.2f} TFLOP/s algorithmic, "
             f"weights read at {rec['weight_stream_gbs']:.0f} GB/s")
+        log(f"  alive after t steps: {', '.join(f'{t}: {n:,}' for t, n in alive.items() if t in ALIVE_AT)}; "
+            f"member-steps in the first 32 steps: {alive['steps_in_first_32']:,}")
     wall, ev, taken, _ = time_rollout(state, theta, hidden, horizon, c, 8, "rows", 1)
     out["static_rows_s8_env_steps_per_s"] = taken / wall
     del theta
