@@ -141,9 +141,9 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
                                         int g = 0, float* xd = nullptr) {
   constexpr int N = 3 + C;
   float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
-  if constexpr (kGroup > 0) {
+  if constexpr (kGroup == 16) {
     // lane g < C evaluates foot g's sin and cos; the group's 16 lanes are one DPP row
-    static_assert(kGroup == 16 && C <= 16, "the group is one 16-lane DPP row");
+    static_assert(C <= 16, "one lane per foot");
     float a = q[2] + q[3];
 #pragma unroll
     for (int k = 1; k < C; ++k) a = (g == k) ? q[2] + q[3 + k] : a;
@@ -234,30 +234,37 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       chol_solve<N>(L, rL, MiJn[k], div);
     }
   } else {
-    static_assert(kGroup >= 2 * C + 1, "one lane per right-hand side");
     constexpr int kRow = 8;  // LDS floats per right-hand side
-    const int rhs = g < 2 * C + 1 ? g : 0;  // lanes past 2C solve the forces again, unused
-    const bool normal = rhs > C;
-    const int k = normal ? rhs - 1 - C : rhs - 1;
-    float ck = ca[0], sk = sa[0];
+    constexpr int kRhs = 2 * C + 1, kRounds = (kRhs + kGroup - 1) / kGroup;
+    float b[kRounds][N];
 #pragma unroll
-    for (int kk = 1; kk < C; ++kk) {
-      ck = (k == kk) ? ca[kk] : ck;
-      sk = (k == kk) ? sa[kk] : sk;
-    }
-    float b[N];
+    for (int r = 0; r < kRounds; ++r) {
+      // lane g solves right-hand sides g, g + kGroup, ...; past 2C it solves the forces again, unused
+      const int rhs = g + r * kGroup < kRhs ? g + r * kGroup : 0;
+      const bool normal = rhs > C;
+      const int k = normal ? rhs - 1 - C : rhs - 1;
+      float ck = ca[0], sk = sa[0];
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const bool on = (i == 2 || i == 3 + k);
-      const float jt = (i == 0) ? 1.0f : on ? ck : 0.0f;
-      const float jn = (i == 1) ? 1.0f : on ? sk : 0.0f;
-      b[i] = (rhs == 0) ? f[i] : normal ? jn : jt;
+      for (int kk = 1; kk < C; ++kk) {
+        ck = (k == kk) ? ca[kk] : ck;
+        sk = (k == kk) ? sa[kk] : sk;
+      }
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const bool on = (i == 2 || i == 3 + k);
+        const float jt = (i == 0) ? 1.0f : on ? ck : 0.0f;
+        const float jn = (i == 1) ? 1.0f : on ? sk : 0.0f;
+        b[r][i] = (rhs == 0) ? f[i] : normal ? jn : jt;
+      }
+      chol_solve<N>(L, rL, b[r], div);
     }
-    chol_solve<N>(L, rL, b, div);
     __syncthreads();  // the rows' previous readers are done
-    if (g < 2 * C + 1) {
 #pragma unroll
-      for (int i = 0; i < N; ++i) xs[g * kRow + i] = b[i];
+    for (int r = 0; r < kRounds; ++r) {
+      if (g + r * kGroup < kRhs) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) xs[(g + r * kGroup) * kRow + i] = b[r][i];
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -273,28 +280,32 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     // lane g < C^2 forms block (g / C, g % C) from the solved rows in xs, and a lane of a
     // diagonal block also forms its contact's ContactBlock; the group reads the C^2 blocks
     // (4 floats each) and the C contact blocks (12 floats each) back from xd
-    static_assert(C * C <= kGroup, "one lane per block");
     constexpr int kRow = 8;
-    const int gb = g < C * C ? g : 0;  // lanes past C^2 form block 0 again, unused
-    const int kb = gb / C, lb = gb % C;
-    float ck = ca[0], sk = sa[0];
+    constexpr int kBlocks = C * C, kRounds = (kBlocks + kGroup - 1) / kGroup;
 #pragma unroll
-    for (int kk = 1; kk < C; ++kk) {
-      ck = (kb == kk) ? ca[kk] : ck;
-      sk = (kb == kk) ? sa[kk] : sk;
-    }
-    const float* rt = xs + (1 + lb) * kRow;
-    const float* rn = xs + (1 + C + lb) * kRow;
-    const float t2 = rt[2], t3 = rt[3 + kb], n2 = rn[2], n3 = rn[3 + kb];
-    const float4 blk4 = make_float4((rt[0] + ck * t2) + ck * t3, (rn[0] + ck * n2) + ck * n3,
-                                    (rt[1] + sk * t2) + sk * t3, (rn[1] + sk * n2) + sk * n3);
-    if (g < C * C) *reinterpret_cast<float4*>(xd + 4 * g) = blk4;
-    const ContactBlock own = contact_block(blk4.x, blk4.y, blk4.w);
-    if (g < C * C && kb == lb) {
-      float* xc = xd + 4 * C * C + 12 * kb;
-      *reinterpret_cast<float4*>(xc) = make_float4(own.det, own.den_p, own.den_m, 0.0f);
-      *reinterpret_cast<double2*>(xc + 4) = make_double2(own.rdet, own.rden_p);
-      *reinterpret_cast<double*>(xc + 8) = own.rden_m;
+    for (int r = 0; r < kRounds; ++r) {
+      const int gr = g + r * kGroup;
+      const int gb = gr < kBlocks ? gr : 0;  // lanes past C^2 form block 0 again, unused
+      const int kb = gb / C, lb = gb % C;
+      float ck = ca[0], sk = sa[0];
+#pragma unroll
+      for (int kk = 1; kk < C; ++kk) {
+        ck = (kb == kk) ? ca[kk] : ck;
+        sk = (kb == kk) ? sa[kk] : sk;
+      }
+      const float* rt = xs + (1 + lb) * kRow;
+      const float* rn = xs + (1 + C + lb) * kRow;
+      const float t2 = rt[2], t3 = rt[3 + kb], n2 = rn[2], n3 = rn[3 + kb];
+      const float4 blk4 = make_float4((rt[0] + ck * t2) + ck * t3, (rn[0] + ck * n2) + ck * n3,
+                                      (rt[1] + sk * t2) + sk * t3, (rn[1] + sk * n2) + sk * n3);
+      if (gr < kBlocks) *reinterpret_cast<float4*>(xd + 4 * gr) = blk4;
+      const ContactBlock own = contact_block(blk4.x, blk4.y, blk4.w);
+      if (gr < kBlocks && kb == lb) {
+        float* xc = xd + 4 * C * C + 12 * kb;
+        *reinterpret_cast<float4*>(xc) = make_float4(own.det, own.den_p, own.den_m, 0.0f);
+        *reinterpret_cast<double2*>(xc + 4) = make_double2(own.rdet, own.rden_p);
+        *reinterpret_cast<double*>(xc + 8) = own.rden_m;
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -564,7 +575,6 @@ template <int C, int HID, int G>
 __device__ __forceinline__ void policy_group(const float* __restrict__ w, const float (&q)[3 + C],
                                              const float (&v)[3 + C], float (&tq)[C], float* xh, float* xl, int g) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
-  static_assert(G >= OUT, "one lane per head");
   using R = UnitRows<OBS, HID, OUT>;
   constexpr int64_t kStride = 64;
   float obs[OBS];
@@ -586,11 +596,13 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
   for (int u = 0; u < (HID + G - 1) / G; ++u)
     if (g + G * u < HID) xh[g + G * u] = hs[u];
   __syncthreads();
-  if (g < OUT) {
-    float lo = w[R::b2(g) * kStride];
+  // lane g sums heads g, g + G, ... over the hidden values in order
+#pragma unroll
+  for (int o = g; o < OUT; o += G) {
+    float lo = w[R::b2(o) * kStride];
 #pragma unroll 8
-    for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w[R::w2(j, g) * kStride];
-    xl[g] = lo;
+    for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w[R::w2(j, o) * kStride];
+    xl[o] = lo;
   }
   __syncthreads();
 #pragma unroll
@@ -786,10 +798,17 @@ constexpr int kGroupLanes = 16;
 #define LEGGED_TAIL_MEMBERS_PER_CU 16  // survivors per CU at the switch: one 4-member wave per SIMD
 #endif
 // Above the tail's bound and up to this many survivors per CU, a chunk runs in the group form
-// (rollout_group_chunk_kernel) instead of one member per lane.
+// (rollout_group_chunk_kernel) instead of one member per lane, with LEGGED_GROUP_CHUNK_LANES
+// lanes per member: 8 lanes and up to 48 per CU (one or two 8-member waves per SIMD, 236
+// registers) beat 16 lanes up to 32 per CU (ES rollout at N = 262,144: 57.2 -> 56.3 ms at 8
+// sweeps, 79.0 -> 77.5 ms at 16); 64 per CU was the same as 48, 32 in between.
 #ifndef LEGGED_GROUP_CHUNK_MEMBERS_PER_CU
-#define LEGGED_GROUP_CHUNK_MEMBERS_PER_CU 32
+#define LEGGED_GROUP_CHUNK_MEMBERS_PER_CU 48
 #endif
+#ifndef LEGGED_GROUP_CHUNK_LANES
+#define LEGGED_GROUP_CHUNK_LANES 8
+#endif
+constexpr int kChunkGroupLanes = LEGGED_GROUP_CHUNK_LANES;
 constexpr int kGroupMembers = 64 / kGroupLanes;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
 template <int C>
@@ -798,7 +817,7 @@ constexpr int kBlockFloats = 4 * C * C + 12 * C;
 // kChunk false: every member runs to the end of its episode. kChunk true: at most chunk_steps
 // steps, then the survivors are appended to dst like rollout_chunk_kernel's (the member's
 // group copies its weight rows).
-template <int C, int HID, bool kChunk>
+template <int C, int HID, int G, bool kChunk>
 __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& dst, int64_t count, int64_t cap,
                                               int32_t chunk_steps, int32_t horizon, int iters, float alive_bonus,
                                               float fall, float gate, float assist, float assist_damping,
@@ -806,7 +825,8 @@ __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& d
                                               float* xs_all, float* xh_all, float* xl_all, float* xd_all) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
-  constexpr int G = kGroupLanes, M = kGroupMembers;
+  constexpr int M = 64 / G;  // members per single-wave workgroup
+  static_assert(G == 8 || G == 16, "groups of 8 or 16 lanes");
   const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
   float* xs = xs_all + mloc * (2 * C + 1) * 8;
   float* xd = xd_all + mloc * kBlockFloats<C>;
@@ -884,11 +904,11 @@ __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& d
 
 // LDS of the group kernels: per member, the solve rows, the Delassus and contact blocks, the
 // hidden values and the head values.
-#define LEGGED_GROUP_LDS(C, HID)                                                   \
-  __shared__ float xs_all[kGroupMembers * (2 * (C) + 1) * 8];                      \
-  __shared__ __align__(16) float xd_all[kGroupMembers * kBlockFloats<(C)>];        \
-  __shared__ float xh_all[kGroupMembers * (HID)];                                  \
-  __shared__ float xl_all[kGroupMembers * 16]
+#define LEGGED_GROUP_LDS(C, HID, M)                                                \
+  __shared__ float xs_all[(M) * (2 * (C) + 1) * 8];                                \
+  __shared__ __align__(16) float xd_all[(M) * kBlockFloats<(C)>];                  \
+  __shared__ float xh_all[(M) * (HID)];                                            \
+  __shared__ float xl_all[(M) * 16]
 
 // The group tail as a kernel of its own, launched after every later chunk: it runs when the
 // set holds at most wide_max members and exits at once otherwise (the chunk kernels do the
@@ -900,14 +920,15 @@ __global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t ca
                                                           float* __restrict__ steps_out, int64_t wide_max) {
   const int64_t count = (int64_t)*src.count;
   if (count > wide_max) return;
-  LEGGED_GROUP_LDS(C, HID);
-  rollout_group<C, HID, false>(src, src, count, cap, horizon, horizon, iters, alive_bonus, fall, gate, assist,
-                               assist_damping, fitness, steps_out, xs_all, xh_all, xl_all, xd_all);
+  LEGGED_GROUP_LDS(C, HID, kGroupMembers);
+  rollout_group<C, HID, kGroupLanes, false>(src, src, count, cap, horizon, horizon, iters, alive_bonus, fall, gate,
+                                            assist, assist_damping, fitness, steps_out, xs_all, xh_all, xl_all,
+                                            xd_all);
 }
 
-// The group form for one chunk, when the set holds more than lo and at most hi members
-// (a few waves of four members per SIMD): the survivors go to dst as after a one-lane chunk.
-template <int C, int HID>
+// The group form for one chunk, G lanes per member, when the set holds more than lo and at
+// most hi members (a wave or two per SIMD): the survivors go to dst as after a one-lane chunk.
+template <int C, int HID, int G>
 __global__ __launch_bounds__(64, 2) void rollout_group_chunk_kernel(Packed src, Packed dst, int64_t cap,
                                                                     int32_t chunk_steps, int32_t horizon, int iters,
                                                                     float alive_bonus, float fall, float gate,
@@ -917,9 +938,9 @@ __global__ __launch_bounds__(64, 2) void rollout_group_chunk_kernel(Packed src, 
                                                                     int64_t hi) {
   const int64_t count = (int64_t)*src.count;
   if (count <= lo || count > hi) return;
-  LEGGED_GROUP_LDS(C, HID);
-  rollout_group<C, HID, true>(src, dst, count, cap, chunk_steps, horizon, iters, alive_bonus, fall, gate, assist,
-                              assist_damping, fitness, steps_out, xs_all, xh_all, xl_all, xd_all);
+  LEGGED_GROUP_LDS(C, HID, 64 / G);
+  rollout_group<C, HID, G, true>(src, dst, count, cap, chunk_steps, horizon, iters, alive_bonus, fall, gate, assist,
+                                 assist_damping, fitness, steps_out, xs_all, xh_all, xl_all, xd_all);
 }
 
 template <int C, int HID, bool kFirst>
@@ -1110,7 +1131,8 @@ inline GroupBounds group_bounds(int64_t p, int cus) {
   // one member group per workgroup: a kernel never holds more than min(p, its bound) members
   const int64_t group_members = p < b.group_max ? p : b.group_max;
   const int64_t tail_members = p < b.wide_max ? p : b.wide_max;
-  b.group_grid = (group_members + kGroupMembers - 1) / kGroupMembers;
+  constexpr int chunk_members = 64 / kChunkGroupLanes;  // per single-wave workgroup
+  b.group_grid = (group_members + chunk_members - 1) / chunk_members;
   b.tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
   return b;
 }
@@ -1127,7 +1149,7 @@ int launch_later_chunk(const float* state0, const float* theta0, int64_t p, cons
                      src, dst, cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
                      gb.group_max);
   if (gb.group_max > gb.wide_max)
-    hipLaunchKernelGGL((rollout_group_chunk_kernel<C, HID>), dim3((unsigned)gb.group_grid), dim3(64), 0, s, src, dst,
+    hipLaunchKernelGGL((rollout_group_chunk_kernel<C, HID, kChunkGroupLanes>), dim3((unsigned)gb.group_grid), dim3(64), 0, s, src, dst,
                        cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps, gb.wide_max,
                        gb.group_max);
   hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)gb.tail_grid), dim3(64), 0, s, src, cap, horizon,

@@ -140,9 +140,10 @@ def test_group_tail_equals_static(dev, c, hidden):
 @pytest.mark.parametrize("c,hidden", [(1, 4), (2, 32), (4, 64)])
 def test_group_chunk_equals_static(dev, c, hidden):
     """Populations of 24 members per CU: above the group tail's bound (16 per CU) and within
-    the group chunk's (32 per CU), so later chunks run in the group form and append their
-    survivors (every chunk, with the assist keeping all members up; until the count falls
-    to the tail's bound, without it): member for member equal to the one-lane kernel."""
+    the group chunk's (48 per CU), so later chunks run in the group form (8 lanes per member:
+    two solves, two Delassus blocks and up to two heads per lane) and append their survivors
+    until the count falls to the tail's bound: member for member equal to the one-lane
+    kernel."""
     from hipenvs import legged, legged_rollout
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
