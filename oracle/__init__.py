@@ -6,7 +6,7 @@ the reference's numpy environments and ES loop (metal-rl-envs:
 ``pendulum_aba_np.py``, ``hopper_np.py``, ``legged_np.py``, ``es.py``), each
 function citing the reference lines it follows. Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
-it, and only as the checker or the timed CPU baseline; the library under
+it, and only to check results against or as the timed CPU baseline; the library under
 ``metal-rl-envs_amd/`` never imports, links or runs anything here, and fails
 loudly when its HIP library is missing.
 

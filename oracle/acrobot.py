@@ -1,6 +1,6 @@
 """Acrobot restated in numpy: the CPU oracle for the HIP Acrobot step and rollout kernels.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 Follows ``acrobot_np.py`` line by line with its Python-scalar groupings kept
 (they decide which constants numpy folds in float64 before rounding to

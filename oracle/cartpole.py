@@ -1,6 +1,6 @@
 """CartPole restated in numpy: the CPU oracle for the HIP step and rollout kernels.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 Follows ``cartpole_np.py`` line by line, in the same float32 operation order
 (numpy's NEP 50 rules turn every Python-float constant into float32 before the

@@ -1,9 +1,9 @@
 """Deterministic float32 sin, cos and tanh, restated in numpy for the oracle.
 
-TEST INFRASTRUCTURE: everything under ``oracle/`` is the CPU checker for the HIP
-library. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg may import it, and only as the checker. The product path
-never calls into it.
+TEST INFRASTRUCTURE: everything under ``oracle/`` is the CPU oracle the HIP
+library's results are checked against. Only ``tests/``, ``__graft_entry__.smoke()``
+and ``bench.py``'s ``cpu_baseline`` leg may import it, and only to check results.
+The product path never calls into it.
 
 Why these exist. The reference evaluates ``np.sin``/``np.cos``/``np.tanh`` on
 float32 arrays (``cartpole_np.py:63``, ``acrobot_np.py:70-77``,

@@ -1,6 +1,6 @@
 """Evolution-strategies pieces restated in numpy for the oracle.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 * ``n_params`` / ``unflatten``: ``es.py:152-164``. A member's row is w1 (I, H)
   row-major, b1 (H), w2 (H, O) row-major, b2 (O).

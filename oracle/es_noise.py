@@ -1,6 +1,6 @@
 """Counter-RNG antithetic Gaussian perturbations and the seeded ES update, restated in numpy.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 The reference's ``generation`` (``es.py:218-227``) draws ``half`` = (P/2, D)
 standard normals from MLX's or numpy's generator, materialises

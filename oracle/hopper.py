@@ -1,6 +1,6 @@
 """The one-contact hopper and the exact single-contact impulse, restated in numpy.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 It is the oracle of the HIP hopper step (the reference's ``hopper_metal``),
 and the legged body reuses its constants and its contact law

@@ -1,7 +1,7 @@
 """The C-legged body with hard contacts, restated in numpy: the CPU oracle for the HIP
 legged step and legged ES rollout kernels.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 Follows ``legged_np.py`` line by line: ``leg_angles``/``static_pose``/
 ``stand_pose`` (30-48), ``torques`` (51-54), ``substep`` (57-97: foot

@@ -1,6 +1,6 @@
 """The K-link pendulum's mass-matrix form, restated in numpy (test oracle for the ABA).
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 Follows ``pendulum_np.py``: constants (29-34), ``hanging_mass`` (37-39), the
 Lagrangian derivative ``Pendulum._dsdt`` (68-79) with K x K mass matrix

@@ -1,7 +1,7 @@
 """The K-link pendulum by the articulated-body algorithm, restated in numpy: the CPU
 oracle for the HIP ABA kernels.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 * ``aba_accelerations`` follows ``pendulum_aba_np.py:30-99`` term by term
   (Featherstone's planar ABA: outward link velocities and velocity-product

@@ -1,6 +1,6 @@
 """The counter-based RNG shared by the oracle and the HIP kernels, restated in numpy.
 
-TEST INFRASTRUCTURE: part of the CPU checker (see ``oracle/__init__.py``).
+TEST INFRASTRUCTURE: part of the CPU oracle (see ``oracle/__init__.py``).
 
 The hash is the PCG hash of Jarzynski & Olano, "Hash Functions for GPU
 Rendering" (JCGT 2020), as the reference's Metal kernels use it

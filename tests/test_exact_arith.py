@@ -52,7 +52,7 @@ def test_every_div_const_divisor_is_declared():
 
 
 @pytest.fixture(scope="module")
-def div_checker(tmp_path_factory):
+def div_check_bin(tmp_path_factory):
     gcc = shutil.which("gcc")
     if gcc is None:
         pytest.skip("gcc not available")
@@ -63,13 +63,13 @@ def div_checker(tmp_path_factory):
 
 
 @pytest.mark.parametrize("literal", sorted({v for vs in div_const_divisors().values() for v in vs}))
-def test_div_const_equals_ieee_division_for_all_floats(div_checker, literal):
-    out = subprocess.run([str(div_checker), literal], capture_output=True, text=True, timeout=600)
+def test_div_const_equals_ieee_division_for_all_floats(div_check_bin, literal):
+    out = subprocess.run([str(div_check_bin), literal], capture_output=True, text=True, timeout=600)
     assert out.returncode == 0 and "mismatches=0" in out.stdout, out.stdout + out.stderr
 
 
-def test_div_const_checker_catches_a_wrong_reciprocal(tmp_path):
-    """The checker is not vacuous: a float32 reciprocal (one extra rounding) fails it."""
+def test_div_const_check_catches_a_wrong_reciprocal(tmp_path):
+    """The exhaustive check is not vacuous: a float32 reciprocal (one extra rounding) fails it."""
     gcc = shutil.which("gcc")
     if gcc is None:
         pytest.skip("gcc not available")
@@ -105,7 +105,7 @@ def test_div_recip_matches_ieee_except_marked_subnormals(tmp_path):
     assert "key_mismatches=0" in out.stdout and " mismatches=0" in out.stdout, out.stdout
 
 
-def test_div_recip_checker_catches_unmarked_subnormals(tmp_path):
+def test_div_recip_check_catches_unmarked_subnormals(tmp_path):
     """Not vacuous: taking the marked subnormal quotients as final answers fails it (the exact
     subnormal midpoints come out wrong)."""
     text = DIV_RECIP_SRC.read_text()

@@ -147,7 +147,7 @@ def test_config0_teacher_forced_1000_steps(dev):
 
 def test_free_running_flags_identical_over_100_steps(dev):
     """Kernel-only chain of 100 steps against the oracle's chain: identical done flags at
-    every step and identical final states (the north-star flag-identity bar)."""
+    every step and identical final states (the flag-identity bar over 100 steps)."""
     from hipenvs import cartpole
 
     n = 4096
