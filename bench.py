@@ -239,6 +239,38 @@ def bench_cartpole(args, dev):
     return value, wall, launch, achieved, fused
 
 
+def copy_floor(n, steps, repeats, dev):
+    """The step's back-to-back launch time against the floor for moving its bytes, at N: an
+    elementwise kernel (torch.neg) that reads and writes 41 B x N / 2 each, replayed
+    `steps` times in a graph like the step, with resident buffers; and the step itself with
+    resident buffers (every launch on action row 0 and reward/done row 0)."""
+    import torch
+
+    elems = CARTPOLE_BYTES * n // 8  # float32 elements: 41 N / 2 bytes read, as many written
+    src = torch.ones(elems, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    g = capture_graph(dev, lambda s: [torch.neg(src, out=dst) for _ in range(steps)])
+    _, ev_copy = time_replay(g, repeats)
+    run = CartPoleRun(n, 1, dev)
+    P = run.lib.ptr
+
+    def body(stream):
+        for t in range(steps):
+            rc = run.fn(P(run.bufs[t % 2]), P(run.actions[0]), run.seed0 + t, P(run.bufs[(t + 1) % 2]),
+                        P(run.rewards[0]), P(run.dones[0]), n, stream)
+            if rc != 0:
+                raise RuntimeError(f"hipenvs_cartpole_step failed: {rc}")
+
+    gs = capture_graph(dev, body)
+    _, ev_step = time_replay(gs, repeats)
+    out = {"n_envs": n, "bytes_per_launch": CARTPOLE_BYTES * n, "copy_us_per_launch": ev_copy / steps * 1e6,
+           "step_resident_us_per_launch": ev_step / steps * 1e6}
+    log(f"N={n}: elementwise copy of the step's bytes {out['copy_us_per_launch']:.3f} us, step with resident "
+        f"buffers {out['step_resident_us_per_launch']:.3f} us per launch")
+    del g, gs, run, src, dst
+    return out
+
+
 def bench_cartpole_at(n, steps, repeats, dev):
     """The same single-step replay at another N (the 2**20 point of the step sweep)."""
     run = CartPoleRun(n, steps, dev)
@@ -776,6 +808,7 @@ def main():
         extra["cartpole_step_us_per_launch"] = launch * 1e6
         if args.n != 1 << 20:
             extra["cartpole_step_n1048576"] = bench_cartpole_at(1 << 20, args.steps, args.repeats, dev)
+        extra["cartpole_copy_floor"] = [copy_floor(m, args.steps, args.repeats, dev) for m in (args.n, 1 << 20)]
         if args.sweep:
             extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out,
                                             0.0 if args.skip_cpu else 0.25)
