@@ -207,6 +207,25 @@ def test_full_size_properties(dev):
     assert 1 / 60 < frac < 1 / 10, frac
 
 
+def test_step_bit_exact_at_the_largest_sweep_size(dev):
+    """N = 2^24, the sweep's largest size (and the 32-bit seed mixing of env indices past
+    2^23): one step from states in the reset range and beyond it (so a share of the envs
+    terminate and reset), every column bit for bit against the oracle."""
+    from hipenvs import cartpole
+
+    n = 1 << 24
+    r = np.random.default_rng(24)
+    state = r.uniform(-0.3, 0.3, size=(4, n)).astype(np.float32)
+    action = r.integers(0, 2, size=n).astype(np.int32)
+    cartpole.reseed(90)
+    ns, rew, done = cartpole.step(torch.from_numpy(state).to(dev), torch.from_numpy(action).to(dev))
+    ens, erew, edone = oc.step(state, action, seed=91)
+    np.testing.assert_array_equal(to_np(done), edone)
+    assert_same_bits(to_np(ns), ens)
+    assert_same_bits(to_np(rew), erew)
+    assert 0.05 < edone.mean() < 0.95
+
+
 def test_resets_vary_and_are_uniform(dev):
     """test_cartpole.py:160-172 on the device."""
     from hipenvs import cartpole
