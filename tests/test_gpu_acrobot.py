@@ -29,6 +29,20 @@ def test_step_matches_oracle_on_random_states(dev, n):
     np.testing.assert_array_equal(to_np(done), edone)
 
 
+def test_step_bit_exact_at_the_benchmark_size(dev):
+    """N = 262,144, the reference's Acrobot step benchmark shape, with mixed terminations."""
+    from hipenvs import acrobot
+
+    state, action = random_batch(1 << 18, seed=18)
+    acrobot.reseed(30)
+    ns, rew, done = acrobot.step(torch.from_numpy(state).to(dev), torch.from_numpy(action).to(dev))
+    ens, erew, edone = oa.step(state, action, seed=31)
+    np.testing.assert_array_equal(to_np(done), edone)
+    np.testing.assert_array_equal(to_np(ns), ens)
+    np.testing.assert_array_equal(to_np(rew), erew)
+    assert 0 < edone.sum() < len(edone)
+
+
 def test_reset_matches_counter_rng(dev):
     from hipenvs import acrobot
 

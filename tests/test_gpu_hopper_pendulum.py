@@ -48,6 +48,20 @@ def test_hopper_step_matches_oracle(dev):
     assert 0 < e_done.sum() < len(e_done)
 
 
+def test_hopper_step_at_the_benchmark_size(dev):
+    """N = 65,536, the bench's hopper step shape."""
+    from hipenvs import hopper
+
+    state, action = hopper_states(1 << 16, seed=16)
+    env = hopper.Hopper()
+    env.reseed(8)
+    nxt, rew, done = env.step(torch.from_numpy(state).to(dev), torch.from_numpy(action).to(dev))
+    e_next, e_rew, e_done = oh.Hopper().step(state, action, 9)
+    np.testing.assert_array_equal(to_np(done), e_done)
+    np.testing.assert_array_equal(to_np(nxt), e_next)
+    np.testing.assert_array_equal(to_np(rew), e_rew)
+
+
 def test_hopper_trajectory_and_reset(dev):
     """100 steps from fresh resets with random actions: identical states and flags."""
     from hipenvs import hopper

@@ -36,6 +36,23 @@ def test_step_matches_oracle(dev, c, iters):
     np.testing.assert_array_equal(to_np(done), edone)
 
 
+def test_step_at_the_benchmark_size(dev):
+    """C = 4, 8 sweeps at N = 65,536, the reference's legged step benchmark shape."""
+    from hipenvs import legged
+
+    state, action = legged_states(4, 1 << 16, seed=16)
+    state[1, :2000] = 0.4  # torsos below the fall height: these terminate and reset
+    state[2, 2000:4000] = 1.3  # and tilted past the fall angle
+    body = legged.Legged(4, 8)
+    body.reseed(5)
+    ns, rew, done = body.step(torch.from_numpy(state).to(dev), torch.from_numpy(action.astype(np.int32)).to(dev))
+    ens, erew, edone = olg.Legged(4, 8).step(state, action, seed=6)
+    np.testing.assert_array_equal(to_np(done), edone)
+    np.testing.assert_array_equal(to_np(ns), ens)
+    np.testing.assert_array_equal(to_np(rew), erew)
+    assert 0 < edone.sum() < len(edone)
+
+
 @pytest.mark.parametrize("c", [2, 4])
 def test_step_with_assist_matches_oracle(dev, c):
     from hipenvs import legged
