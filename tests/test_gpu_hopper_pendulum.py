@@ -98,6 +98,21 @@ def test_pendulum_step_matches_oracle(dev, k):
     np.testing.assert_array_equal(to_np(nxt), e_next)
 
 
+def test_pendulum_step_at_the_benchmark_size(dev):
+    """K = 16 at N = 65,536, the bench's largest mass-matrix pendulum shape."""
+    from hipenvs import pendulum
+
+    state, action = pendulum_states(16, 1 << 16, seed=16)
+    env = pendulum.Pendulum(16)
+    env.reseed(20)
+    nxt, rew, done = env.step(torch.from_numpy(state).to(dev), torch.from_numpy(action).to(dev))
+    e_next, e_rew, e_done = op.Pendulum(16).step(state, action, 21)
+    np.testing.assert_array_equal(to_np(done), e_done)
+    np.testing.assert_array_equal(to_np(nxt), e_next)
+    np.testing.assert_array_equal(to_np(rew), e_rew)
+    assert 0 < e_done.sum() < len(e_done)
+
+
 @pytest.mark.parametrize("k", [2, 4, 16])
 def test_pendulum_trajectory(dev, k):
     from hipenvs import pendulum
