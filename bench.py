@@ -77,13 +77,13 @@ FP32_PEAK_TFLOPS = 157.3           # MI355X FP32 vector, packed (published)
 FP32_UNPACKED_TFLOPS = 78.6        # one FMA per lane per cycle
 CARTPOLE_BYTES = 41
 # HBM bytes per cartpole_step launch: rocprofv3 --pmc FETCH_SIZE and then WRITE_SIZE over
-# `bench.py --only cartpole --copy-mib 256` read 2579.5 / 5378.5 KiB per dispatch at N = 2**18
-# and 10259.6 / 21692.4 KiB at N = 2**20; the same counters read 131085.2 and 262144.0 KiB
+# `bench.py --only cartpole --copy-mib 256` read 2580.5 / 5377.2 KiB per dispatch at N = 2**18
+# and 10260.5 / 21649.5 KiB at N = 2**20; the same counters read 131085.2 and 262144.0 KiB
 # for the 256 MiB device copy in the same process, so they are scaled by 2.000 and 1.000.
 # Commands and tables: profiles/cartpole_step_n262144.md. Algorithmic bytes: 41 x N.
 _FETCH_SCALE = 262144.0 / 131085.2
 CARTPOLE_TRAFFIC = {n: int(round((fetch * _FETCH_SCALE + write) * 1024))
-                    for n, fetch, write in ((1 << 18, 2579.5, 5378.5), (1 << 20, 10259.6, 21692.4))}
+                    for n, fetch, write in ((1 << 18, 2580.5, 5377.2), (1 << 20, 10260.5, 21649.5))}
 
 
 def log(msg):
