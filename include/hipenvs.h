@@ -6,7 +6,8 @@
  * every buffer (device memory, fp32 structure-of-arrays state of shape
  * (rows, n), row-major, contiguous); the library allocates nothing, frees
  * nothing and keeps no per-call state, so any host thread may call it on any
- * stream. Inputs are never written.
+ * stream (the one exception, hipenvs_es_update_static, keeps its partial sums
+ * in a static device array). Inputs are never written.
  *
  * Return value: HIPENVS_OK (0), or a negative HIPENVS_E_* code. On
  * HIPENVS_E_HIP the launch failed and hipenvs_last_hip_error() gives the
@@ -35,7 +36,8 @@ enum {
   HIPENVS_OK = 0,
   HIPENVS_E_ARG = -1,         /* null pointer with n > 0, negative size, bad parameter */
   HIPENVS_E_UNSUPPORTED = -2, /* a compile-time shape (hidden, K links, C legs) with no instantiation */
-  HIPENVS_E_HIP = -3          /* the HIP launch failed; see hipenvs_last_hip_error() */
+  HIPENVS_E_HIP = -3,         /* the HIP launch failed; see hipenvs_last_hip_error() */
+  HIPENVS_E_SCRATCH = -4      /* the shape needs more than a static-scratch entry point holds */
 };
 
 /* Library version and build description, e.g. "hipenvs 0.1 gfx950 fp-contract=off". */
@@ -293,6 +295,23 @@ int64_t hipenvs_es_update_workspace_bytes(int64_t d, int64_t p);
 int hipenvs_es_update(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed, double sigma,
                       double lr, float* theta_out, void* workspace, int64_t workspace_bytes,
                       hipenvs_stream_t stream);
+
+/* Bytes of the static device array behind hipenvs_es_update_static (2 MiB: the partial
+ * sums of any population at d <= 2048, which covers every task's policy up to hidden 64). */
+#define HIPENVS_ES_UPDATE_STATIC_BYTES (2 * 1024 * 1024)
+
+/* hipenvs_es_update without a workspace argument and without any allocation: the
+ * partial sums go to a file-scope device array of HIPENVS_ES_UPDATE_STATIC_BYTES that
+ * each GPU holds until the process ends (its address is looked up once per device, on
+ * the first call with that device current). Same results as hipenvs_es_update.
+ * Returns HIPENVS_E_SCRATCH when hipenvs_es_update_workspace_bytes(d, p) exceeds the
+ * array. Calls on one GPU share the array: calls that overlap on one GPU (different
+ * streams, or host threads) race and must be ordered by the caller.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+int hipenvs_es_update_static(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed,
+                             double sigma, double lr, float* theta_out, hipenvs_stream_t stream);
 
 /* hipenvs_cartpole_es_rollout on the population of hipenvs_es_perturb (rows),
  * which is written to workspace (workspace_bytes >= 4 * p * (7*hidden+2)) and

@@ -2,6 +2,9 @@
 // theta + lr * sum_m rank_m eps_m / (P sigma), with eps regenerated from the counter RNG
 // (es_noise.h) instead of stored. Replaces the noise lines of the reference's generation
 // (es.py:218-226): no (P, D) noise tensor, no (P, D) product in the update.
+#include <atomic>
+#include <mutex>
+
 #include "es_noise.h"
 
 namespace hipenvs {
@@ -128,15 +131,12 @@ extern "C" int64_t hipenvs_es_update_workspace_bytes(int64_t d, int64_t p) {
   return (int64_t)sizeof(float) * esn::update_chunks(p / 2) * d;
 }
 
-extern "C" int hipenvs_es_update(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed,
-                                 double sigma, double lr, float* theta_out, void* workspace,
-                                 int64_t workspace_bytes, hipenvs_stream_t stream) {
-  if (!population_ok(d, p) || !theta || !ranks || !theta_out || !workspace) return HIPENVS_E_ARG;
-  if (workspace_bytes < hipenvs_es_update_workspace_bytes(d, p)) return HIPENVS_E_ARG;
-  hipStream_t s = as_stream(stream);
+namespace {
+// The update's two launches with its partial sums in `partial` (update_chunks(p / 2) x d floats).
+int launch_update(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed, double sigma,
+                  double lr, float* theta_out, float* partial, hipStream_t s) {
   const int64_t half = p / 2, mc = esn::chunk_members(half), chunks = esn::update_chunks(half);
   const uint32_t pairs = (uint32_t)((d + 1) / 2);
-  float* partial = static_cast<float*>(workspace);
   hipLaunchKernelGGL(esn::noise_partial_kernel, dim3((pairs + 63) / 64, (unsigned)chunks), dim3(64), 0, s, ranks, d,
                      (uint32_t)half, pairs, seed, (uint32_t)mc, partial);
   int status = launch_status();
@@ -146,4 +146,65 @@ extern "C" int hipenvs_es_update(const float* theta, const float* ranks, int64_t
   hipLaunchKernelGGL(esn::update_kernel, dim3(grid_for(d)), dim3(kBlock), 0, s, theta, partial, d, (uint32_t)chunks,
                      scale, (float)lr, theta_out);
   return launch_status();
+}
+
+// Static partial-sum buffer of hipenvs_es_update_static: each GPU the library runs on holds
+// its own copy until the process ends. Host code never uses the array's name as an address
+// (on the host it is only a stand-in for the device symbol); it uses the device address that
+// hipGetSymbolAddress returns, looked up once per device with that device current.
+constexpr int64_t kStaticPartialFloats = HIPENVS_ES_UPDATE_STATIC_BYTES / (int64_t)sizeof(float);
+__device__ __align__(256) float scratch[kStaticPartialFloats];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// The current device's address of `scratch`, or a negative status.
+int static_partials(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_last_hip_error((int)e);
+    return HIPENVS_E_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return HIPENVS_E_ARG;
+  float* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !addr) {
+        set_last_hip_error((int)(e != hipSuccess ? e : hipErrorInvalidSymbol));
+        return HIPENVS_E_HIP;
+      }
+      ptr = static_cast<float*>(addr);
+      g_scratch[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return HIPENVS_OK;
+}
+}  // namespace
+
+extern "C" int hipenvs_es_update(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed,
+                                 double sigma, double lr, float* theta_out, void* workspace,
+                                 int64_t workspace_bytes, hipenvs_stream_t stream) {
+  if (!population_ok(d, p) || !theta || !ranks || !theta_out || !workspace) return HIPENVS_E_ARG;
+  if (workspace_bytes < hipenvs_es_update_workspace_bytes(d, p)) return HIPENVS_E_ARG;
+  return launch_update(theta, ranks, d, p, seed, sigma, lr, theta_out, static_cast<float*>(workspace),
+                       as_stream(stream));
+}
+
+extern "C" int hipenvs_es_update_static(const float* theta, const float* ranks, int64_t d, int64_t p, uint32_t seed,
+                                        double sigma, double lr, float* theta_out, hipenvs_stream_t stream) {
+  if (!population_ok(d, p) || !theta || !ranks || !theta_out) return HIPENVS_E_ARG;
+  if (hipenvs_es_update_workspace_bytes(d, p) > HIPENVS_ES_UPDATE_STATIC_BYTES) return HIPENVS_E_SCRATCH;
+  float* partial = nullptr;
+  const int status = static_partials(&partial);
+  if (status != HIPENVS_OK) return status;
+  // every partial the update kernel reads is written first by the partial kernel of the same
+  // call, so nothing is cleared
+  return launch_update(theta, ranks, d, p, seed, sigma, lr, theta_out, partial, as_stream(stream));
 }

@@ -16,7 +16,10 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libhipenvs.so")
 
-OK, E_ARG, E_UNSUPPORTED, E_HIP = 0, -1, -2, -3
+OK, E_ARG, E_UNSUPPORTED, E_HIP, E_SCRATCH = 0, -1, -2, -3, -4
+
+# bytes of the static device array behind hipenvs_es_update_static (HIPENVS_ES_UPDATE_STATIC_BYTES)
+ES_UPDATE_STATIC_BYTES = 2 * 1024 * 1024
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -55,6 +58,7 @@ SIGNATURES = {
     "hipenvs_legged_evaluate": [_I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _P, _P],
     "hipenvs_es_perturb": [_P, _I64, _I64, _U32, ctypes.c_double, _I32, _P, _P],
     "hipenvs_es_update": [_P, _P, _I64, _I64, _U32, ctypes.c_double, ctypes.c_double, _P, _P, _I64, _P],
+    "hipenvs_es_update_static": [_P, _P, _I64, _I64, _U32, ctypes.c_double, ctypes.c_double, _P, _P],
     "hipenvs_cartpole_es_rollout_seeded": [_P, _P, _I64, _U32, ctypes.c_double, _I32, _I32, _P, _P, _I64, _P],
     "hipenvs_acrobot_es_rollout_seeded": [_P, _P, _I64, _U32, ctypes.c_double, _I32, _I32, _P, _P, _I64, _P],
     "hipenvs_legged_es_rollout_seeded": [_I32, _I32, _I32, _I32, _P, _P, _I64, _U32, ctypes.c_double, _I32, _F32,
@@ -106,6 +110,8 @@ def call(name, *args):
             raise HipEnvsError(f"{name}: HIP launch failed (hipError_t {lib().hipenvs_last_hip_error()})")
         if rc == E_UNSUPPORTED:
             raise HipEnvsError(f"{name}: no kernel instantiated for these compile-time parameters")
+        if rc == E_SCRATCH:
+            raise HipEnvsError(f"{name}: the shape needs more than the library's static scratch holds")
         raise HipEnvsError(f"{name}: invalid argument (status {rc})")
 
 

@@ -43,8 +43,7 @@ def perturb(theta, p, seed, sigma, layout="rows"):
     return out
 
 
-def update(theta, ranks, seed, sigma, lr):
-    """theta + lr * (sum_m ranks[m] eps[m]) / (P sigma) with the noise of ``seed``; ranks (P,) float32."""
+def _update_args(theta, ranks):
     if not isinstance(theta, torch.Tensor) or theta.dim() != 1:
         raise TypeError("theta must be a 1-D torch.Tensor")
     d = theta.shape[0]
@@ -53,6 +52,27 @@ def update(theta, ranks, seed, sigma, lr):
         raise TypeError("ranks must be a 1-D torch.Tensor")
     p = _lib.check_population(ranks.shape[0])
     ranks = _lib.as_f32_vector(ranks, p, theta.device, "ranks")
+    return theta, ranks, d, p
+
+
+def update_static(theta, ranks, seed, sigma, lr, out):
+    """``update`` into the caller's ``out`` (d,) with no device allocation: the partial sums
+    live in the library's static 2 MiB device array (d <= 2048 at any population), which
+    calls on one GPU share, so overlapping calls race. For capture and serving loops."""
+    theta, ranks, d, p = _update_args(theta, ranks)
+    out_ok = (isinstance(out, torch.Tensor) and out.dtype == torch.float32 and out.shape == (d,)
+              and out.device == theta.device and out.is_contiguous())
+    if not out_ok:
+        raise ValueError(f"out must be a contiguous float32 ({d},) tensor on {theta.device}")
+    with torch.cuda.device(theta.device):
+        _lib.call("hipenvs_es_update_static", _lib.ptr(theta), _lib.ptr(ranks), d, p, _lib.u32(seed), float(sigma),
+                  float(lr), _lib.ptr(out), _lib.stream_of(theta.device))
+    return out
+
+
+def update(theta, ranks, seed, sigma, lr):
+    """theta + lr * (sum_m ranks[m] eps[m]) / (P sigma) with the noise of ``seed``; ranks (P,) float32."""
+    theta, ranks, d, p = _update_args(theta, ranks)
     nbytes = _lib.lib().hipenvs_es_update_workspace_bytes(d, p)
     if nbytes < 0:
         raise _lib.HipEnvsError(f"hipenvs_es_update: unsupported population ({p}, {d})")
