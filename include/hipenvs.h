@@ -207,6 +207,19 @@ int hipenvs_legged_step(int32_t c, int32_t iters, double assist, const float* st
                         uint32_t seed, const float* stand, float* next_state, float* reward, uint8_t* done,
                         int64_t n, hipenvs_stream_t stream);
 
+/* The same control step in the reference's own arithmetic: legged_np.Legged.step
+ * (legged_np.py:57-132) as numpy evaluates it. numpy makes the contact solve's
+ * tangential impulse float64 (hopper_np.py:100) and promotes the velocities and the
+ * state with it, so the next state is float64 (d, n) and a float64 state runs every
+ * substep in float64; from a float32 state the first substep is float32 up to its
+ * first contact solve. state is float32 (state_is_f64 == 0) or float64 (1);
+ * next_state (2(3+c), n) f64; reward (v_x + 1 rounded to f32, 0 on a fall) and done
+ * as hipenvs_legged_step, same reset. c in {1, 2, 3, 4}, iters 1..4096. The parity
+ * path for the reference's numpy; hipenvs_legged_step is the Metal kernel's float32. */
+int hipenvs_legged_step_reference(int32_t c, int32_t iters, double assist, const void* state, int32_t state_is_f64,
+                                  const int32_t* action, uint32_t seed, const float* stand, double* next_state,
+                                  float* reward, uint8_t* done, int64_t n, hipenvs_stream_t stream);
+
 /* Fused ES rollout on the legged body: one thread per member runs its
  * (5+2c)-H-3c tanh policy (one three-way head per leg) and the physics for up
  * to `horizon` steps; fitness (p) = sum of ((v_x if y >= height_gate else 0) +

@@ -114,6 +114,44 @@ __device__ __forceinline__ void det_sincos(float x, float* sin_out, float* cos_o
   *cos_out = ((q + 1) & 2) ? -b : b;
 }
 
+// Deterministic float64 sin/cos, for the reference-precision legged step (the reference's
+// numpy evaluates np.sin/np.cos on float64 arrays once its state has been promoted).
+// Cody-Waite reduction by pi/2 in three float64 pieces (33 + 33 + 53 significant bits, so
+// k * PIO2_D1 and k * PIO2_D2 are exact for |k| < 2^20), then the Taylor series of sin to
+// r^19 and of cos to r^20 (coefficients 1/n! rounded to float64). Every argument takes the
+// same operations; NaN and infinities give NaN. Within 1.7 ulp of the exact values for
+// |x| < 2^20 pi/2.
+namespace dm {
+constexpr double PIO2_D1 = 0x1.921fb54400000p+0;
+constexpr double PIO2_D2 = 0x1.0b4611a600000p-34;
+constexpr double PIO2_D3 = 0x1.3198a2e037073p-69;
+constexpr double TWO_OVER_PI_64 = 0x1.45f306dc9c883p-1;
+constexpr double SIN64_C[9] = {-0x1.5555555555555p-3, 0x1.1111111111111p-7, -0x1.a01a01a01a01ap-13,
+                               0x1.71de3a556c734p-19, -0x1.ae64567f544e4p-26, 0x1.6124613a86d09p-33,
+                               -0x1.ae7f3e733b81fp-41, 0x1.952c77030ad4ap-49, -0x1.2f49b46814157p-57};
+constexpr double COS64_C[10] = {-0x1.0000000000000p-1, 0x1.5555555555555p-5, -0x1.6c16c16c16c17p-10,
+                                0x1.a01a01a01a01ap-16, -0x1.27e4fb7789f5cp-22, 0x1.1eed8eff8d898p-29,
+                                -0x1.93974a8c07c9dp-37, 0x1.ae7f3e733b81fp-45, -0x1.6827863b97d97p-53,
+                                0x1.e542ba4020225p-62};
+}  // namespace dm
+
+__device__ __forceinline__ void det_sincos64(double x, double* sin_out, double* cos_out) {
+  const double k = __builtin_rint(x * dm::TWO_OVER_PI_64);
+  const double r = ((x - k * dm::PIO2_D1) - k * dm::PIO2_D2) - k * dm::PIO2_D3;
+  const double z = r * r;
+  double sp = dm::SIN64_C[8];
+#pragma unroll
+  for (int i = 7; i >= 0; --i) sp = dm::SIN64_C[i] + z * sp;
+  const double s = r + (r * z) * sp;
+  double cp = dm::COS64_C[9];
+#pragma unroll
+  for (int i = 8; i >= 0; --i) cp = dm::COS64_C[i] + z * cp;
+  const double c = 1.0 + z * cp;
+  const double q = k - 4.0 * __builtin_floor(k * 0.25);  // 0..3 exactly for finite k; NaN otherwise
+  *sin_out = (q == 0.0) ? s : (q == 1.0) ? c : (q == 2.0) ? -s : -c;
+  *cos_out = (q == 0.0) ? c : (q == 1.0) ? -s : (q == 2.0) ? -c : s;
+}
+
 // det_sincos for arguments that are usually near zero (CartPole's pole angle). When every
 // active lane of the wave has |x| <= 0.78, rint(x * 2/pi) is 0 on every lane, the reduction
 // returns x itself (a zero of either sign gives the same sin and cos), and the quadrant is

@@ -45,6 +45,7 @@ SIGNATURES = {
     "hipenvs_pendulum_aba_accelerations": [_I32, _P, _P, _P, _I64, _P],
     "hipenvs_legged_reset": [_I32, _P, _P, _I64, _U32, _P],
     "hipenvs_legged_step": [_I32, _I32, ctypes.c_double, _P, _P, _U32, _P, _P, _P, _P, _I64, _P],
+    "hipenvs_legged_step_reference": [_I32, _I32, ctypes.c_double, _P, _I32, _P, _U32, _P, _P, _P, _P, _I64, _P],
     "hipenvs_legged_es_rollout": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32, ctypes.c_double,
                                   _P, _P, _P],
     "hipenvs_legged_es_rollout_chunked": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32,
@@ -136,12 +137,13 @@ def ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
-def check_state(state, rows, name="state"):
-    """A (rows, n) float32 contiguous tensor on a GPU; returns n."""
+def check_state(state, rows, name="state", dtypes=(torch.float32,)):
+    """A (rows, n) contiguous tensor on a GPU of one of `dtypes` (float32 by default); returns n."""
     if not isinstance(state, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor, got {type(state).__name__}")
-    if state.dtype != torch.float32:
-        raise TypeError(f"{name} must be float32, got {state.dtype}")
+    if state.dtype not in dtypes:
+        names = " or ".join(str(d).replace("torch.", "") for d in dtypes)
+        raise TypeError(f"{name} must be {names}, got {state.dtype}")
     if state.dim() != 2 or state.shape[0] != rows:
         raise ValueError(f"{name} must have shape ({rows}, n), got {tuple(state.shape)}")
     if state.device.type != "cuda":

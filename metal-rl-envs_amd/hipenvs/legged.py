@@ -10,6 +10,13 @@ with ``iters`` sweeps of block projected Gauss-Seidel over the C contacts,
 reward forward velocity + 1 (0 on a fall), terminated columns reset to the
 standing pose plus U[+-0.05] noise from the counter RNG. C in {1, 2, 3, 4}.
 ``reset(n, seed=None)`` replaces ``legged_mlx.Legged.reset``.
+
+``precision="reference"`` runs ``legged_np``'s own arithmetic instead of the Metal
+kernel's float32: numpy promotes the tangential impulse to float64 in its contact
+solve (``hopper_np.py:100``), and with it the velocities and the state, so
+``legged_np.Legged.step`` returns a float64 state and every later step runs in
+float64. In this mode ``step`` takes a float32 or float64 state and returns a
+float64 one, with the same dtype flow (iters >= 1).
 """
 
 import numpy as np
@@ -42,12 +49,21 @@ def stand_pose(c):
     return np.concatenate([q, np.zeros_like(q)]).astype(np.float32)
 
 
+PRECISIONS = ("f32", "reference")
+
+
 class Legged:
-    def __init__(self, c, iters=ITERS):
+    def __init__(self, c, iters=ITERS, precision="f32"):
         if int(c) not in SUPPORTED_C:
             raise ValueError(f"c must be one of {SUPPORTED_C}, got {c}")
         if not 0 <= int(iters) <= 4096:
             raise ValueError("iters must be in [0, 4096]")
+        if precision not in PRECISIONS:
+            raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
+        if precision == "reference" and int(iters) < 1:
+            raise ValueError("precision='reference' needs iters >= 1 (with no sweep the reference never leaves "
+                             "float32: use precision='f32')")
+        self.precision = precision
         self.c, self.iters = int(c), int(iters)
         self.n_actions = 3 ** self.c
         self.rows = 2 * (3 + self.c)
@@ -79,6 +95,8 @@ class Legged:
     def step(self, state, action, assist=None):
         """All N envs by one control step (four substeps) in one launch, asynchronously.
         ``assist`` (a float) is the torso spring-damper stiffness of the curriculum."""
+        if self.precision == "reference":
+            return self._step_reference(state, action, assist)
         n = _lib.check_state(state, self.rows)
         device = state.device
         action = _lib.as_actions(action, n, device)
@@ -90,4 +108,19 @@ class Legged:
             _lib.call("hipenvs_legged_step", self.c, self.iters, float(assist or 0.0), _lib.ptr(state),
                       _lib.ptr(action), _lib.u32(self.calls), _lib.ptr(self.stand_on(device)), _lib.ptr(next_state),
                       _lib.ptr(reward), _lib.ptr(done), n, _lib.stream_of(device))
+        return next_state, reward, done
+
+    def _step_reference(self, state, action, assist):
+        is_f64 = int(isinstance(state, torch.Tensor) and state.dtype == torch.float64)
+        n = _lib.check_state(state, self.rows, dtypes=(torch.float32, torch.float64))
+        device = state.device
+        action = _lib.as_actions(action, n, device)
+        self.calls += 1
+        next_state = torch.empty((self.rows, n), dtype=torch.float64, device=device)
+        reward = torch.empty(n, dtype=torch.float32, device=device)
+        done = torch.empty(n, dtype=torch.bool, device=device)
+        with torch.cuda.device(device):
+            _lib.call("hipenvs_legged_step_reference", self.c, self.iters, float(assist or 0.0), _lib.ptr(state),
+                      is_f64, _lib.ptr(action), _lib.u32(self.calls), _lib.ptr(self.stand_on(device)),
+                      _lib.ptr(next_state), _lib.ptr(reward), _lib.ptr(done), n, _lib.stream_of(device))
         return next_state, reward, done

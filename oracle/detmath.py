@@ -36,7 +36,7 @@ bound the distance to numpy's own float32 functions, which is what ties this
 oracle to the reference's arithmetic.
 
 The HIP twin of every function here is in
-``metal-rl-envs_amd/csrc/hipenvs_math.h``; a GPU test checks the two
+``metal-rl-envs_amd/csrc/hipenvs_device.h``; a GPU test checks the two
 bit-for-bit over a million arguments.
 """
 
@@ -133,7 +133,7 @@ def _poly(r):
 
 
 def sincos(x):
-    """(sin x, cos x) as float32 arrays, bit-identical to det_sincos in hipenvs_math.h."""
+    """(sin x, cos x) as float32 arrays, bit-identical to det_sincos in hipenvs_device.h."""
     r, q = _reduce(x)
     with np.errstate(invalid="ignore", over="ignore"):
         s, c = _poly(r)
@@ -169,7 +169,7 @@ def expm1_nonneg(y):
 
 
 def tanh(x):
-    """float32 tanh, bit-identical to det_tanh in hipenvs_math.h."""
+    """float32 tanh, bit-identical to det_tanh in hipenvs_device.h."""
     x = np.asarray(x, dtype=F32)
     a = np.abs(x)
     with np.errstate(invalid="ignore"):
@@ -179,11 +179,81 @@ def tanh(x):
     return np.copysign(t, x).astype(F32)
 
 
+# ---------------------------------------------------------------------------
+# Deterministic float64 sin/cos, for the float64 arithmetic the reference's legged
+# body falls into (its numpy promotes the state to float64; legged_np.py:66 then
+# evaluates np.cos/np.sin on float64 arrays). Same construction as the float32 pair:
+# Cody-Waite reduction by pi/2 in three float64 pieces (33 + 33 + 53 significant
+# bits: k * D1 and k * D2 exact for |k| < 2**20), then the Taylor series of sin to
+# r**19 and of cos to r**20 on |r| <= pi/4 (truncation below 2**-70 relative), with
+# plain float64 operations and no fused multiply-add, so the GPU reproduces every bit.
+# ---------------------------------------------------------------------------
+
+def _constants64():
+    from fractions import Fraction
+    pio2 = Fraction(PI_DIGITS) / 2
+
+    def head33(v):
+        b = np.array(float(v), dtype=np.float64).view(np.uint64)
+        return float((b & ~np.uint64((1 << 20) - 1)).view(np.float64))
+
+    d1 = head33(pio2)
+    d2 = head33(pio2 - Fraction(d1))
+    d3 = float(pio2 - Fraction(d1) - Fraction(d2))
+    sin_c = tuple(float(Fraction((-1) ** i, math.factorial(2 * i + 1))) for i in range(1, 10))   # r**3 .. r**19
+    cos_c = tuple(float(Fraction((-1) ** i, math.factorial(2 * i))) for i in range(1, 11))       # r**2 .. r**20
+    return np.float64(d1), np.float64(d2), np.float64(d3), sin_c, cos_c
+
+
+PIO2_D1, PIO2_D2, PIO2_D3, SIN64_C, COS64_C = _constants64()
+TWO_OVER_PI_64 = np.float64(2.0 / math.pi)
+CONSTANT_HEX.update({"PIO2_D1": float(PIO2_D1).hex(), "PIO2_D2": float(PIO2_D2).hex(),
+                     "PIO2_D3": float(PIO2_D3).hex(), "TWO_OVER_PI_64": float(TWO_OVER_PI_64).hex()})
+
+
+def sincos64(x):
+    """(sin x, cos x) as float64 arrays, bit-identical to det_sincos64 in hipenvs_device.h.
+    Any float64 x: the same operations run for every argument (accurate for |x| < 2**20 * pi/2;
+    NaN and infinities give NaN)."""
+    x = np.asarray(x, dtype=np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        k = np.rint(x * TWO_OVER_PI_64)
+        r = ((x - k * PIO2_D1) - k * PIO2_D2) - k * PIO2_D3
+        z = r * r
+        sp = np.float64(SIN64_C[-1])
+        for c in SIN64_C[-2::-1]:
+            sp = c + z * sp
+        s = r + (r * z) * sp
+        cp = np.float64(COS64_C[-1])
+        for c in COS64_C[-2::-1]:
+            cp = c + z * cp
+        co = 1.0 + z * cp
+        q = k - 4.0 * np.floor(k * 0.25)
+    sin_v = np.where(q == 0.0, s, np.where(q == 1.0, co, np.where(q == 2.0, -s, -co)))
+    cos_v = np.where(q == 0.0, co, np.where(q == 1.0, -s, np.where(q == 2.0, -co, s)))
+    return sin_v, cos_v
+
+
+def _by_dtype(f32_fn, f64_fn):
+    def fn(x):
+        x = np.asarray(x)
+        return f64_fn(x) if x.dtype == np.float64 else f32_fn(x)
+    return fn
+
+
+sin_by_dtype = _by_dtype(sin, lambda x: sincos64(x)[0])
+cos_by_dtype = _by_dtype(cos, lambda x: sincos64(x)[1])
+
+
 def trig_functions(kind):
     """(sin, cos, tanh) callables for the oracle: 'det' (bit-identical to the HIP
-    kernels, the default) or 'numpy' (the reference's own np.sin/np.cos/np.tanh)."""
+    kernels, the default), 'det64' (det on float32 arrays, sincos64 on float64 ones:
+    the HIP reference-precision legged step) or 'numpy' (the reference's own
+    np.sin/np.cos/np.tanh)."""
     if kind == "det":
         return sin, cos, tanh
+    if kind == "det64":
+        return sin_by_dtype, cos_by_dtype, tanh
     if kind == "numpy":
         return np.sin, np.cos, np.tanh
     raise ValueError(f"unknown trig kind {kind!r}")

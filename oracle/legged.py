@@ -118,8 +118,8 @@ def substep(q, v, torque, c, iters=ITERS, mu=MU, assist=0.0, mode="f32", trig=No
 class Legged:
     """``legged_np.Legged`` (``legged_np.py:105-132``) with counter-RNG resets."""
 
-    def __init__(self, c, iters=ITERS, mode="f32"):
-        self.c, self.iters, self.mode = c, iters, mode
+    def __init__(self, c, iters=ITERS, mode="f32", trig=None):
+        self.c, self.iters, self.mode, self.trig = c, iters, mode, trig
         self.n_actions = 3**c
         self.stand = stand_pose(c)
 
@@ -132,14 +132,14 @@ class Legged:
         q, v = state[:d], state[d:]
         tq = torques(action, self.c)
         for _ in range(SUBSTEPS):
-            q, v = substep(q, v, tq, self.c, self.iters, assist=assist, mode=self.mode)
+            q, v = substep(q, v, tq, self.c, self.iters, assist=assist, mode=self.mode, trig=self.trig)
         return np.concatenate([q, v])
 
     def physics_torques(self, state, tq, assist=0.0):
         d = 3 + self.c
         q, v = state[:d], state[d:]
         for _ in range(SUBSTEPS):
-            q, v = substep(q, v, tq, self.c, self.iters, assist=assist, mode=self.mode)
+            q, v = substep(q, v, tq, self.c, self.iters, assist=assist, mode=self.mode, trig=self.trig)
         return q, v
 
     @staticmethod
@@ -147,9 +147,12 @@ class Legged:
         return (state[1] < FALL_HEIGHT) | (np.abs(state[2]) > FALL_ANGLE)
 
     def step(self, state, action, seed, assist=0.0):
-        """``legged_np.py:114-121``: reward forward velocity + 1, 0 on done."""
+        """``legged_np.py:114-121``: reward forward velocity + 1, 0 on done. In the f32 mode the
+        state is float32 throughout; in the reference mode a float32 state is promoted as the
+        reference promotes it and the next state is float64, like legged_np's."""
         n = state.shape[1]
-        stepped = self.physics(np.asarray(state, dtype=F32), action, assist)
+        state = np.asarray(state)
+        stepped = self.physics(state.astype(F32) if self.mode == "f32" else state, action, assist)
         done = self.terminated(stepped)
         fresh = self.reset(n, seed)
         next_state = np.where(done[None, :], fresh, stepped)

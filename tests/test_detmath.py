@@ -86,3 +86,53 @@ def test_header_constants_match_the_oracle():
         m = re.search(rf"\b{name} = (-?0x[0-9a-fA-F.]+p[+-]?\d+)f", text)
         assert m, name
         assert float.fromhex(m.group(1)) == float(value), name
+    for name, values in (("SIN64_C", dm.SIN64_C), ("COS64_C", dm.COS64_C)):
+        m = re.search(rf"constexpr double {name}\[\d+\] = \{{([^}}]*)\}};", text)
+        assert m, name
+        got = [float.fromhex(v.strip()) for v in m.group(1).split(",")]
+        assert got == [float(v) for v in values], name
+
+
+def _ulp64(got, exact):
+    import mpmath
+
+    out = []
+    for g, t in zip(got, exact):
+        out.append(0.0 if t == 0 and g == 0 else float(abs(mpmath.mpf(float(g)) - t) / np.spacing(abs(float(t)))))
+    return np.array(out)
+
+
+def test_sincos64_against_exact_values():
+    """The float64 pair (reference-precision legged step) within 2 ulp of the exact sin/cos
+    (mpmath at 200 bits) on the legged body's angle range and far beyond it."""
+    import mpmath
+
+    mpmath.mp.prec = 200
+    rng = np.random.default_rng(64)
+    x = np.concatenate([rng.uniform(-4, 4, 3000), rng.uniform(-1e4, 1e4, 1000), rng.uniform(-1e-6, 1e-6, 200),
+                        [0.0, np.pi / 4, np.pi / 2, 3.0, 1e-300]])
+    s, c = dm.sincos64(x)
+    assert s.dtype == np.float64 and c.dtype == np.float64
+    es = _ulp64(s, [mpmath.sin(mpmath.mpf(float(v))) for v in x])
+    ec = _ulp64(c, [mpmath.cos(mpmath.mpf(float(v))) for v in x])
+    assert es.max() <= 2.0 and ec.max() <= 2.0, (es.max(), ec.max())
+    assert es.mean() < 0.5 and ec.mean() < 0.5
+
+
+def test_sincos64_close_to_numpy_and_special_values():
+    x = np.random.default_rng(65).uniform(-8, 8, 1_000_000)
+    s, c = dm.sincos64(x)
+    assert np.max(np.abs(s - np.sin(x)) / np.spacing(np.abs(np.sin(x)))) <= 2.0
+    assert np.max(np.abs(c - np.cos(x)) / np.spacing(np.abs(np.cos(x)))) <= 2.0
+    s, c = dm.sincos64(np.array([np.nan, np.inf, -np.inf]))
+    assert np.isnan(s).all() and np.isnan(c).all()
+
+
+def test_trig_by_dtype_dispatch():
+    """'det64' evaluates float32 arrays with the float32 functions and float64 arrays with
+    sincos64, as numpy's np.sin keeps each array's dtype."""
+    sin_f, cos_f, _ = dm.trig_functions("det64")
+    x32 = np.linspace(-3, 3, 101, dtype=np.float32)
+    assert np.array_equal(sin_f(x32), dm.sin(x32)) and sin_f(x32).dtype == np.float32
+    x64 = x32.astype(np.float64)
+    assert np.array_equal(cos_f(x64), dm.sincos64(x64)[1]) and cos_f(x64).dtype == np.float64
