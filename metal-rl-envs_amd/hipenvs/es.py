@@ -13,7 +13,7 @@ Kept from the reference:
 * ``loop_fitness``'s accounting (``es.py:174-193``), ``push``/``curriculum``
   (``es.py:196-211``), ``centered_ranks`` (``es.py:214-215``, with ties broken
   by index: a stable sort), ``generation`` (``es.py:218-227``), ``evaluate``
-  (``es.py:308-322``) and ``train`` (``es.py:334-354``).
+  (``es.py:308-322``) and the stopping rule of ``train`` (``es.py:334-354``).
 
 Backends (``es.py:230-299``): ``"fused"`` runs the whole rollout as one HIP
 launch per generation (the reference's ``metal`` backend); ``"loop"`` runs the
@@ -26,7 +26,6 @@ the rollout and update kernels (``es_noise``), so neither the (P, D) noise nor
 the population is ever a tensor; ranking stays a torch sort.
 """
 
-import argparse
 import time
 from dataclasses import dataclass
 from typing import Any, Callable
@@ -361,54 +360,63 @@ class Result:
     score: float
 
 
-def train(cfg, backend_name, seed, log=lambda *_: None, device=None):
-    """Generations until the mean policy's score reaches the threshold or the time budget
-    runs out (``es.py:334-354``); evaluation is outside the clock."""
-    assert cfg.pop % 2 == 0
-    task = TASKS[cfg.task]
-    hidden = task.hidden if cfg.hidden is None else cfg.hidden
-    solved_at = task.solved_at if cfg.solved_at is None else cfg.solved_at
-    backend = BACKENDS[backend_name](task, seed, device)
-    theta = backend.normal((n_params(hidden, task),)) * 0.1
-    train_seconds, env_steps, score, gen = 0.0, 0, 0.0, 0
-    for gen in range(1, cfg.max_generations + 1):
-        torch.cuda.synchronize(backend.device)
+@dataclass
+class GenerationLog:
+    generation: int
+    env_steps: int        # steps taken so far, summed over members and generations
+    train_seconds: float  # device time of the generations so far
+    pop_fitness: float    # mean training fitness of this generation's population
+    score: float          # the mean policy's canonical score after this generation
+
+
+class Trainer:
+    """One ES run: its backend, the current parameters and the running totals. ``advance()``
+    runs a generation between two device synchronisations (the training clock) and scores
+    the updated mean policy after the clock stops."""
+
+    def __init__(self, cfg, backend_name, seed, device=None):
+        if cfg.pop % 2:
+            raise ValueError("the population must be even (antithetic pairs)")
+        self.cfg = cfg
+        self.task = TASKS[cfg.task]
+        self.hidden = self.task.hidden if cfg.hidden is None else cfg.hidden
+        self.threshold = self.task.solved_at if cfg.solved_at is None else cfg.solved_at
+        self.backend = BACKENDS[backend_name](self.task, seed, device)
+        self.theta = self.backend.normal((n_params(self.hidden, self.task),)) * 0.1   # initial policy (es.py:340)
+        self.history = []
+        self._seconds, self._steps = 0.0, 0
+
+    def advance(self):
+        gen = len(self.history) + 1
+        dev = self.backend.device
+        torch.cuda.synchronize(dev)
         start = time.perf_counter()
-        theta, fit, steps = generation(backend, theta, cfg, hidden, gen)
-        torch.cuda.synchronize(backend.device)
-        train_seconds += time.perf_counter() - start
-        env_steps += int(steps.sum().item())
-        score = evaluate_theta(task, theta, hidden, device=backend.device)
-        log(gen, env_steps, train_seconds, float(fit.mean().item()), score)
-        if score >= solved_at:
-            return Result(True, gen, env_steps, train_seconds, score)
-        if train_seconds >= cfg.time_budget:
-            break
-    return Result(False, gen, env_steps, train_seconds, score)
+        self.theta, fit, steps = generation(self.backend, self.theta, self.cfg, self.hidden, gen)
+        torch.cuda.synchronize(dev)
+        self._seconds += time.perf_counter() - start
+        self._steps += int(steps.sum().item())
+        score = evaluate_theta(self.task, self.theta, self.hidden, device=dev)
+        record = GenerationLog(gen, self._steps, self._seconds, float(fit.mean().item()), score)
+        self.history.append(record)
+        return record
+
+    @property
+    def solved(self):
+        return bool(self.history) and self.history[-1].score >= self.threshold
+
+    @property
+    def exhausted(self):
+        return len(self.history) >= self.cfg.max_generations or self._seconds >= self.cfg.time_budget
 
 
-def main():
-    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--task", choices=sorted(TASKS), default="cartpole")
-    p.add_argument("--pop", type=int, default=1024)
-    p.add_argument("--backend", choices=BACKENDS, default="fused")
-    p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--lr", type=float, default=0.1)
-    p.add_argument("--sigma", type=float, default=0.1)
-    p.add_argument("--time-budget", type=float, default=120.0)
-    p.add_argument("--max-generations", type=int, default=500)
-    p.add_argument("--assist", type=float, default=0.0)
-    p.add_argument("--start-velocity", type=float, default=0.0)
-    p.add_argument("--anneal", type=int, default=300)
-    a = p.parse_args()
-    cfg = Config(task=a.task, pop=a.pop, lr=a.lr, sigma=a.sigma, time_budget=a.time_budget,
-                 max_generations=a.max_generations, assist_k0=a.assist, start_velocity=a.start_velocity,
-                 anneal_gens=a.anneal)
-    result = train(cfg, a.backend, a.seed, log=lambda gen, es_, secs, fit, score: print(
-        f"gen {gen:4d}  env_steps {es_:>13,}  train {secs:7.2f}s  pop fitness {fit:8.1f}  score {score:8.1f}",
-        flush=True))
-    print(result)
-
-
-if __name__ == "__main__":
-    main()
+def train(cfg, backend_name, seed, log=None, device=None):
+    """Generations until the mean policy's score reaches the task's threshold, the generation
+    cap or the training-time budget (the reference's ``train``, ``es.py:334-354``).
+    ``log(generation, env_steps, train_seconds, pop_fitness, score)`` is called after each."""
+    trainer = Trainer(cfg, backend_name, seed, device)
+    while True:
+        rec = trainer.advance()
+        if log is not None:
+            log(rec.generation, rec.env_steps, rec.train_seconds, rec.pop_fitness, rec.score)
+        if trainer.solved or trainer.exhausted:
+            return Result(trainer.solved, rec.generation, rec.env_steps, rec.train_seconds, rec.score)

@@ -50,3 +50,14 @@ def test_es_learns_acrobot(dev):
     r = es.train(es.Config(task="acrobot", pop=4096, time_budget=30.0, solved_at=-250.0, max_generations=100),
                  "fused", seed=0, device=dev)
     assert r.score >= -250.0, r
+
+
+@pytest.mark.parametrize("backend", ["fused", "seeded"])
+def test_es_learns_to_stay_up_on_two_legs(dev, backend):
+    """test_es.py:124-131: a random biped falls in about 20 steps (training fitness ~20 under
+    the alive bonus); within 60 generations of 1,024 members the population's training
+    fitness reaches 300 (standing is worth about 500)."""
+    last = []
+    es.train(es.Config(task="legged2", pop=1024, time_budget=30.0, max_generations=60), backend, seed=0,
+             device=dev, log=lambda gen, steps, secs, fit, score: last.append(fit))
+    assert last[-1] >= 300.0, last

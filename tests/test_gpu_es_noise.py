@@ -142,21 +142,24 @@ def test_bad_populations_are_rejected(dev):
     assert l.hipenvs_cartpole_es_rollout_seeded(null, null, 4, 0, 0.1, 32, 10, null, null, 0, null) == _lib.E_ARG
 
 
-def test_config4_full_size_schedules_agree(dev):
-    """At the benchmark's full shape (legged4, N = 262,144, H = 64, S = 8, horizon 1,000,
-    sigma 0.03 around 0.1 N(0, 1)): the seeded rollout, the chunked rollout of the perturbed
-    columns and the one-member-per-lane rollout of the perturbed rows agree member for member."""
+@pytest.mark.parametrize("c,iters", [(4, 4), (4, 8), (4, 16), (2, 4), (2, 8), (2, 16)])
+def test_config4_full_size_schedules_agree(dev, c, iters):
+    """At the benchmark's full shape (N = 262,144, H = 64, horizon 1,000, sigma 0.03 around
+    0.1 N(0, 1)) for the quadruped and the biped at S = 4, 8, 16: the seeded rollout, the
+    chunked rollout of the perturbed columns and the one-member-per-lane rollout of the
+    perturbed rows agree member for member."""
     from hipenvs import es_noise, legged, legged_rollout
 
-    p, hidden, c = 262_144, 64, 4
+    p, hidden = 262_144, 64
+    print(f"config-4 full size c={c} iters={iters}", flush=True)
     theta = torch.from_numpy(theta0(legged_rollout.n_params(hidden, c), 2024)).to(dev)
     state = legged.Legged(c).reset(p, seed=0, device=dev)
-    fs, ss = legged_rollout.rollout_seeded(state, theta, 5, 0.03, hidden, 1000, c)
+    fs, ss = legged_rollout.rollout_seeded(state, theta, 5, 0.03, hidden, 1000, c, iters=iters)
     cols = es_noise.perturb(theta, p, 5, 0.03, layout="columns")
-    fc, sc = legged_rollout.rollout(state, None, hidden, 1000, c, theta_cols=cols)
+    fc, sc = legged_rollout.rollout(state, None, hidden, 1000, c, theta_cols=cols, iters=iters)
     del cols
     rows = es_noise.perturb(theta, p, 5, 0.03)
-    fr, sr = legged_rollout.rollout(state, rows, hidden, 1000, c, schedule="rows")
+    fr, sr = legged_rollout.rollout(state, rows, hidden, 1000, c, schedule="rows", iters=iters)
     assert torch.equal(fs, fc) and torch.equal(ss, sc)
     assert torch.equal(fs, fr) and torch.equal(ss, sr)
     assert sr.max().item() == 1000 or sr.max().item() > 300  # a long tail reaches the group phase

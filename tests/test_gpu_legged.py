@@ -92,21 +92,25 @@ def _population(p, c, hidden, scale, seed):
     return (r.standard_normal((p, legged_rollout.n_params(hidden, c))) * scale).astype(np.float32)
 
 
-@pytest.mark.parametrize("c,hidden,p,horizon", [(1, 8, 128, 60), (2, 16, 256, 100), (4, 64, 96, 40)])
-def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon):
+@pytest.mark.parametrize("iters", [4, 8, 16])
+@pytest.mark.parametrize("c,hidden,p,horizon", [(1, 8, 128, 60), (2, 16, 256, 100), (2, 64, 96, 40),
+                                                 (4, 64, 96, 40)])
+def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon, iters):
+    """Every schedule at the benchmark's sweep counts S = 4, 8, 16, including the biped and
+    the quadruped at H = 64."""
     from hipenvs import legged, legged_rollout
 
     theta = _population(p, c, hidden, 0.3, c)
     state = olg.Legged(c).reset(p, seed=7)
     st, th = torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev)
-    fk, sk = legged_rollout.rollout(st, th, hidden, horizon, c)
-    ef, es_ = olg.rollout_fused(state, theta, hidden, horizon, c)
+    fk, sk = legged_rollout.rollout(st, th, hidden, horizon, c, iters=iters)
+    ef, es_ = olg.rollout_fused(state, theta, hidden, horizon, c, iters=iters)
     np.testing.assert_array_equal(to_np(fk), ef)
     np.testing.assert_array_equal(to_np(sk), es_)
-    fc, sc = legged_rollout.rollout(st, th.T.contiguous(), hidden, horizon, c, schedule="columns")
+    fc, sc = legged_rollout.rollout(st, th.T.contiguous(), hidden, horizon, c, schedule="columns", iters=iters)
     np.testing.assert_array_equal(to_np(fc), ef)
     np.testing.assert_array_equal(to_np(sc), es_)
-    fr, sr = legged_rollout.rollout(st, th, hidden, horizon, c, schedule="rows")
+    fr, sr = legged_rollout.rollout(st, th, hidden, horizon, c, schedule="rows", iters=iters)
     np.testing.assert_array_equal(to_np(fr), ef)
     np.testing.assert_array_equal(to_np(sr), es_)
     assert 1 <= es_.mean() <= horizon
@@ -134,8 +138,9 @@ def test_chunked_schedule_at_scale_equals_static(dev):
     assert torch.equal(fq, fs) and torch.equal(sq, ss)
 
 
-@pytest.mark.parametrize("c,hidden", [(1, 4), (1, 64), (2, 8), (2, 32), (4, 4), (4, 64)])
-def test_group_tail_equals_static(dev, c, hidden):
+@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (1, 64, 8), (2, 8, 8), (2, 32, 8), (4, 4, 8), (4, 64, 8),
+                                            (2, 64, 4), (2, 64, 16), (4, 64, 4), (4, 64, 16)])
+def test_group_tail_equals_static(dev, c, hidden, iters):
     """Populations that the compacting schedule hands to its group tail (a lane group per
     member) after the first chunk, at every leg count and hidden width the group code
     distinguishes (one to four hidden units per lane, 2C + 1 solve lanes, 3C head lanes),
@@ -148,14 +153,15 @@ def test_group_tail_equals_static(dev, c, hidden):
     state = legged.Legged(c).reset(p, seed=5, device=dev)
     for assist in (0.0, 20.0):
         fq, sq = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="chunked",
-                                        chunk_steps=8)
-        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="rows")
+                                        chunk_steps=8, iters=iters)
+        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="rows",
+                                        iters=iters)
         assert torch.equal(fq, fs) and torch.equal(sq, ss), (c, hidden, assist)
         assert ss.max().item() > 8  # members outlived the first chunk
 
 
-@pytest.mark.parametrize("c,hidden", [(1, 4), (2, 32), (4, 64)])
-def test_group_chunk_equals_static(dev, c, hidden):
+@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (2, 32, 8), (4, 64, 8), (2, 64, 4), (4, 64, 16)])
+def test_group_chunk_equals_static(dev, c, hidden, iters):
     """Populations of 24 members per CU: above the group tail's bound (16 per CU) and within
     the group chunk's (48 per CU), so later chunks run in the group form (8 lanes per member:
     two solves, two Delassus blocks and up to two heads per lane) and append their survivors
@@ -170,8 +176,9 @@ def test_group_chunk_equals_static(dev, c, hidden):
     for assist, scale in ((0.0, 0.3), (20.0, 0.0)):
         theta = torch.from_numpy(_population(p, c, hidden, scale, 7 * c + hidden)).to(dev)
         fq, sq = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="chunked",
-                                        chunk_steps=8)
-        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="rows")
+                                        chunk_steps=8, iters=iters)
+        fs, ss = legged_rollout.rollout(state, theta, hidden, horizon, c, assist=assist, schedule="rows",
+                                        iters=iters)
         assert torch.equal(fq, fs) and torch.equal(sq, ss), (c, hidden, assist)
         past_first = max(past_first, int((ss > 8).sum().item()))
     assert past_first > 16 * cus  # the second chunk ran in the group form
@@ -221,3 +228,27 @@ def test_fused_rollout_close_to_the_oracle_loop(dev):
     close = np.abs(fk - fl) <= 1e-3 * np.maximum(np.abs(fl), 1.0) + 1e-2
     assert close.mean() > 0.95 and (sk == sl).mean() > 0.95, (close.mean(), (sk == sl).mean())
     assert 5 < sl.mean() < 200
+
+
+@pytest.mark.parametrize("c", [2, 4])
+@pytest.mark.parametrize("iters", [4, 8, 16])
+def test_config4_population_matches_oracle(dev, c, iters):
+    """The benchmark's population at small P: H = 64, sigma 0.03 antithetic around
+    theta0 = 0.1 N(0, 1), alive bonus 1 + forward velocity, S = 4/8/16, for the biped and the
+    quadruped: the seeded rollout against the oracle's fused restatement on the oracle's own
+    perturbation, member for member."""
+    from hipenvs import legged_rollout
+    from oracle import es_noise as oen
+
+    p, hidden, horizon = 128, 64, 120
+    d = legged_rollout.n_params(hidden, c)
+    theta = (np.random.default_rng(2024 + c).standard_normal(d) * 0.1).astype(np.float32)
+    pop = oen.perturb(theta, p, 31 + iters, 0.03)
+    state = olg.Legged(c).reset(p, seed=9)
+    print(f"config-4 population c={c} iters={iters}", flush=True)
+    fk, sk = legged_rollout.rollout_seeded(torch.from_numpy(state).to(dev), torch.from_numpy(theta).to(dev),
+                                           31 + iters, 0.03, hidden, horizon, c, iters=iters)
+    ef, es_ = olg.rollout_fused(state, pop, hidden, horizon, c, iters=iters)
+    np.testing.assert_array_equal(to_np(sk), es_)
+    np.testing.assert_array_equal(to_np(fk), ef)
+    assert es_.min() < es_.max()
