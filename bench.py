@@ -1,40 +1,50 @@
 """Benchmark of the hipenvs hot path on one MI355X; prints ONE JSON line on stdout
 (progress goes to stderr).
 
-Headline (`value`): the batched CartPole step at N = 2**18 environments with the
-reference's step-kernel API (one launch per env step, cartpole_metal.step),
-`--steps` timed steps (default 1,000) after `--warmup` untimed ones. The timed
-launches are captured once into a HIP graph outside the clock and replayed, so
-the clock measures the kernels, not Python. Inputs (state and the pre-drawn
-Bernoulli(0.5) actions of every step) are resident in HBM before the clock
-starts; every step's reward and done rows are written to a (steps, N) rollout
-buffer, as the reference's harness materialises them (bench.py:48-61).
+Headline (`value`): the batched CartPole step at N = 2**18 environments under the
+reference's timing rule (bench.py:48-61, README:135-172): every iteration samples the
+actions on the device (Bernoulli(0.5) from the counter RNG, hipenvs_sample_actions)
+and then steps (hipenvs_cartpole_step, the cartpole_metal.step API), and every step's
+reward and done rows are kept, as the reference's harness materialises them. The
+`--steps` iterations are captured once into a HIP graph outside the clock; a timed
+region replays that graph `repeats_per_region` times back to back between two device
+synchronisations (enough replays for a region of about 0.25 s, so short `--steps`
+runs still measure the steady state); env-steps/s = N x steps x replays / wall
+seconds, median of `--repeats` regions; `ms_per_step` = wall / (steps x replays).
 
-Timing rule (the reference's, bench.py:75-82 / README:135-172): env-steps/s =
-N x timed steps / wall seconds, device synchronised before and after the timed
-region, median of `--repeats` repeats.
-
-`roofline` (cartpole_step): achieved = 41 algorithmic bytes per env-step (16 B
-state in, 4 B action, 16 B state out, 4 B reward, 1 B done) x N / the average
-launch duration, which is the HIP-event time of the timed replay (events on
-the replay's stream) divided by its launches; peak 8 TB/s HBM.
+`roofline` (the dominant kernel, cp::step_kernel): achieved = 41 algorithmic bytes
+per env-step (16 B state in, 4 B action, 16 B state out, 4 B reward, 1 B done) x N /
+the kernel's average duration in the rocprofv3 kernel trace of this command
+(profiles/cartpole_step_n262144.md; the tracer runs every dispatch on its own);
+`achieved_events` / `frac_events` are the same bytes over the back-to-back launch
+time measured live here with HIP events on the replay stream, on a graph of the
+step alone with pre-drawn actions; `traffic` is the counter-measured HBM bytes per
+launch (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size).
 
 `cpu_baseline`: the CPU oracle's numpy CartPole step (the reference's algorithm
 and op order with np.sin/np.cos, one process) at the same N for a bounded
 sample of about `--cpu-seconds` seconds on this host.
 
 `extra` holds the rest of the workload list, measured in the same run:
-* `legged4_es_rollout`: the fused legged ES rollout at N = 262,144 members,
-  C = 4 legs, H = 64, sigma 0.03 antithetic around theta0 = 0.1 N(0, 1), alive
-  bonus 1 + forward velocity, horizon 1,000, S = 4/8/16 Gauss-Seidel sweeps:
+* `legged4_es_rollout`, `legged2_es_rollout`: the fused legged ES rollout at
+  N = 262,144 members, C = 4 legs (quadruped) and C = 2 (biped), H = 64, sigma 0.03
+  antithetic around theta0 = 0.1 N(0, 1), alive bonus 1 + forward velocity,
+  horizon 1,000, S = 4/8/16 Gauss-Seidel sweeps:
   compacting chunked schedule, env-steps (steps taken) per second, a VALU roofline from the algorithmic
   FLOP count of the kernel source, and the numpy reference path (oracle in
   the reference's literal arithmetic: einsum policy + legged_np step) timed
   on a bounded sample of steps at the same N;
+* `cartpole_step_kernel_only`: the step alone on actions drawn before the clock (the
+  previous headline form), and `cartpole_module_api`: the drop-in module calls
+  (hipenvs.cartpole.sample_actions + hipenvs.cartpole.step) from a Python loop, the
+  rate a caller of the reference's API sees without graph capture;
+* `cartpole_step_n1048576`, `cartpole_step_n16777216`: the step alone at 2^20 and at
+  2^24 (a working set far beyond the 256 MB last-level cache: HBM-bound);
 * `cartpole_fused_k32`: the K = 32 fused CartPole step, in-kernel and array actions;
 * `es_config2`: CartPole and Acrobot fused ES rollouts, P = 4,096, H = 32, horizon 500,
-  with the reference's numpy ES loop (all members stepped every iteration) timed beside
-  them in member-steps/s, to compare with the GPU's P x horizon rate;
+  with a VALU roofline from the kernel source's FLOP count per step taken, and the
+  reference's numpy ES loop (all members stepped every iteration) timed beside them in
+  member-steps/s, to compare with the GPU's P x horizon rate;
 * `aba_euler`: the K-link pendulum, semi-implicit Euler dt 0.01, N = 65,536,
   K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B) and the
   numpy ABA Euler step timed beside it;
@@ -49,13 +59,15 @@ sample of about `--cpu-seconds` seconds on this host.
 * `step_bodies`: single-step kernels graph-replayed for 1,000 steps with actions drawn on
   the device: the mass-matrix K-link pendulum (K = 2/4/8/16, RK4 dt 0.02) and the hopper at
   N = 65,536; the Acrobot step at N = 262,144; the legged C = 4 step with 8 sweeps at
-  N = 65,536 (uniform actions in [0, 81)) -- the reference's own step benchmarks' shapes;
+  N = 65,536 (uniform actions in [0, 81)) -- the reference's own step benchmarks' shapes --
+  and the same legged step in the reference's precision (float64 state);
 * `es_evaluate`: the learner's greedy evaluation of the mean policy (es.py:308-322,
   2,048 envs x 500 steps): the fused one-launch kernel against the reference's
   loop (torch mean policy + one env-step launch per iteration); wall time, median
   of repeats, and both scores.
 
-Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--sweep] [--skip-cpu] [--only cartpole|legged]
+Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--repeats 3] [--sweep] [--skip-cpu]
+                      [--only cartpole|legged]
 """
 
 import argparse
@@ -86,6 +98,15 @@ CARTPOLE_TRAFFIC = {n: int(round((fetch * _FETCH_SCALE + write) * 1024))
                     for n, fetch, write in ((1 << 18, 2580.5, 5377.2), (1 << 20, 10260.5, 21649.5))}
 
 
+# HBM bytes per launch of the ABA Euler step at N = 65,536 and per rollout of the legged ES
+# rollout at N = 262,144 (all of its chunk and tail kernels), keyed by K and by (C, S):
+# FETCH_SIZE + WRITE_SIZE from rocprofv3 --pmc runs of `bench.py --only legged` / the ABA
+# block, scaled like CARTPOLE_TRAFFIC; profiles/aba_euler_n65536.md and
+# profiles/legged_es_rollout_n262144.md hold the tables. None where not collected.
+ABA_TRAFFIC = {}
+LEGGED_ROLLOUT_TRAFFIC = {}
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -97,11 +118,15 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--n", type=int, default=1 << 18)
     p.add_argument("--repeats", type=int, default=3)
+    p.add_argument("--region-seconds", type=float, default=0.25,
+                   help="length of a timed region of the headline: graph replays back to back")
     p.add_argument("--fused-k", type=int, default=32)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--legged-cpu-seconds", type=float, default=12.0)
     p.add_argument("--skip-cpu", action="store_true")
-    p.add_argument("--only", choices=["cartpole", "legged"], default=None)
+    p.add_argument("--only", choices=["cartpole", "legged", "aba"], default=None,
+                   help="run one block: the CartPole headline, the legged rollouts (then the line's value is the "
+                        "legged4 S = 8 rollout), or the ABA Euler step (for counter collection; no line)")
     p.add_argument("--legged-n", type=int, default=262144)
     p.add_argument("--legged-horizon", type=int, default=1000)
     p.add_argument("--sweep", action="store_true", help="also run the CartPole N = 2^0..2^24 sweep")
@@ -155,6 +180,26 @@ class CartPoleRun:
     def graph_single(self):
         return capture_graph(self.dev, lambda s: [self.launch_step(t, s) for t in range(self.steps)])
 
+    def graph_sampled(self):
+        """Per iteration: the device sampler draws step t's actions into one (N,) row, then the
+        step consumes them (the reference's loop samples inside the timed region)."""
+        P = self.lib.ptr
+        sampler = self.lib.lib().hipenvs_sample_actions
+        row = self.torch.empty(self.n, dtype=self.torch.int32, device=self.dev)
+
+        def body(stream):
+            for t in range(self.steps):
+                rc = sampler(P(row), self.n, 2, self.seed0 + t, stream)
+                if rc != 0:
+                    raise RuntimeError(f"hipenvs_sample_actions failed: {rc}")
+                rc = self.fn(P(self.bufs[t % 2]), P(row), self.seed0 + t, P(self.bufs[(t + 1) % 2]),
+                             P(self.rewards[t]), P(self.dones[t]), self.n, stream)
+                if rc != 0:
+                    raise RuntimeError(f"hipenvs_cartpole_step failed: {rc}")
+
+        self.sample_row = row
+        return capture_graph(self.dev, body)
+
     def graph_fused(self, k, array_actions):
         def body(s):
             t = 0
@@ -181,8 +226,9 @@ def capture_graph(dev, body):
     return g
 
 
-def time_replay(g, repeats):
-    """(median wall s, median HIP-event s) of graph replays; events on the replay's stream."""
+def time_replay(g, repeats, per_region=1):
+    """(median wall s, median HIP-event s) of timed regions, each `per_region` graph replays
+    back to back between two device synchronisations; events on the replay's stream."""
     import torch
 
     g.replay()
@@ -193,7 +239,8 @@ def time_replay(g, repeats):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record()
-        g.replay()
+        for _ in range(per_region):
+            g.replay()
         end.record()
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
@@ -201,7 +248,15 @@ def time_replay(g, repeats):
     return statistics.median(walls), statistics.median(events)
 
 
+def replays_for(g, seconds):
+    """Graph replays that fill a timed region of about `seconds` (at least one)."""
+    wall, _ = time_replay(g, 1)
+    return max(1, int(round(seconds / max(wall, 1e-9))))
+
+
 def bench_cartpole(args, dev):
+    """The headline: device action sampler + step per iteration (the reference's rule), then
+    the step alone on pre-drawn actions and the K-fused step."""
     import torch
 
     from hipenvs import _lib
@@ -212,12 +267,20 @@ def bench_cartpole(args, dev):
     for t in range(warmup):
         run.launch_step(t % steps, stream)
     torch.cuda.synchronize()
-    g = run.graph_single()
-    wall, ev = time_replay(g, args.repeats)
-    value = n * steps / wall
-    launch = ev / steps
-    achieved = CARTPOLE_BYTES * n / launch / 1e9
-    log(f"cartpole_step N={n}: {value:,.0f} env-steps/s; {launch * 1e6:.3f} us per launch -> {achieved:.1f} GB/s")
+    g = run.graph_sampled()
+    per_region = replays_for(g, args.region_seconds)
+    wall, ev = time_replay(g, args.repeats, per_region)
+    iterations = steps * per_region
+    value = n * iterations / wall
+    log(f"cartpole sampler + step N={n}: {value:,.0f} env-steps/s; {wall / iterations * 1e6:.3f} us per iteration "
+        f"({per_region} replays of {steps} steps per region)")
+    gk1 = run.graph_single()
+    wall1, ev1 = time_replay(gk1, args.repeats, per_region)
+    launch = ev1 / iterations
+    kernel_only = {"env_steps_per_s": n * iterations / wall1, "us_per_launch_events": launch * 1e6,
+                   "achieved_gbs_events": CARTPOLE_BYTES * n / launch / 1e9}
+    log(f"cartpole_step alone (actions drawn before the clock) N={n}: {kernel_only['env_steps_per_s']:,.0f} "
+        f"env-steps/s; {launch * 1e6:.3f} us per launch -> {kernel_only['achieved_gbs_events']:.1f} GB/s")
     gk = run.graph_fused(args.fused_k, False)
     wk, evk = time_replay(gk, args.repeats)
     gka = run.graph_fused(args.fused_k, True)
@@ -235,8 +298,62 @@ def bench_cartpole(args, dev):
     }
     log(f"cartpole fused K={k}: in-kernel actions {fused['inkernel_actions_env_steps_per_s']:,.0f}, "
         f"array actions {fused['array_actions_env_steps_per_s']:,.0f} env-steps/s")
-    del g, gk, gka, run
-    return value, wall, launch, achieved, fused
+    del g, gk1, gk, gka, run
+    return {"value": value, "wall": wall, "iterations": iterations, "per_region": per_region,
+            "us_per_iteration": wall / iterations * 1e6, "kernel_only": kernel_only, "fused": fused}
+
+
+def module_api_rate(n, steps, dev):
+    """The drop-in modules called from a Python loop (no graph): per iteration
+    hipenvs.cartpole.sample_actions then hipenvs.cartpole.step, every reward and done kept
+    until one synchronisation at the end (the reference's mlx_rollout, bench.py:48-61)."""
+    import torch
+
+    from hipenvs import cartpole
+
+    def loop(count, seed0):
+        state = cartpole.reset(n, seed=0, device=dev)
+        pending = []
+        for t in range(count):
+            state, reward, done = cartpole.step(state, cartpole.sample_actions(n, seed=seed0 + t, device=dev))
+            pending += [reward, done]
+        return state, pending
+
+    loop(16, 1)
+    torch.cuda.synchronize()
+    walls = []
+    for r in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loop(steps, 100 + r * steps)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+    wall = statistics.median(walls)
+    out = {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_iteration": wall / steps * 1e6}
+    log(f"cartpole module API loop N={n}: {out['env_steps_per_s']:,.0f} env-steps/s, "
+        f"{out['us_per_iteration']:.2f} us per iteration")
+    return out
+
+
+# Average duration of cp::step_kernel per dispatch in the rocprofv3 kernel trace of the
+# default command (`bench.py`, all of whose step launches at a given N are traced), in ns;
+# profiles/cartpole_step_n262144.md tabulates them. The tracer runs each dispatch on its own,
+# so these include the per-dispatch ramp and drain that back-to-back launches overlap.
+CARTPOLE_TRACE_NS = {1 << 18: 3349.0, 1 << 20: 8159.0}
+
+
+def cartpole_roofline(n, kernel_only):
+    """HBM roofline of cp::step_kernel at N: primary from the kernel trace's average duration,
+    secondary from this run's back-to-back HIP-event launch time."""
+    bytes_launch = CARTPOLE_BYTES * n
+    events_gbs = kernel_only["achieved_gbs_events"]
+    trace_ns = CARTPOLE_TRACE_NS.get(n)
+    achieved = bytes_launch / (trace_ns * 1e-9) / 1e9 if trace_ns else events_gbs
+    return {"bound": "hbm", "kernel": "cp::step_kernel", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(n),
+            "algorithmic_bytes_per_launch": bytes_launch, "avg_launch_ns_trace": trace_ns,
+            "avg_launch_ns_events": kernel_only["us_per_launch_events"] * 1e3,
+            "achieved_events": events_gbs, "frac_events": events_gbs / HBM_PEAK_GBS}
 
 
 def copy_floor(n, steps, repeats, dev):
@@ -272,7 +389,8 @@ def copy_floor(n, steps, repeats, dev):
 
 
 def bench_cartpole_at(n, steps, repeats, dev):
-    """The same single-step replay at another N (the 2**20 point of the step sweep)."""
+    """The step alone (pre-drawn actions), graph-replayed, at another N (the 2**20 and 2**24
+    points of the step sweep)."""
     run = CartPoleRun(n, steps, dev)
     wall, ev = time_replay(run.graph_single(), repeats)
     launch = ev / steps
@@ -421,10 +539,10 @@ def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats, al
 ALIVE_AT = (32, 64, 96, 128, 160, 192, 224, 256, 512, 999)
 
 
-def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
+def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
     from hipenvs import legged, legged_rollout
 
-    c, hidden, p, horizon = 4, 64, args.legged_n, args.legged_horizon
+    hidden, p, horizon = 64, args.legged_n, args.legged_horizon
     theta = legged_population(dev, p, c, hidden)
     theta_cols = theta.T.contiguous()
     state = legged.Legged(c).reset(p, seed=0, device=dev)
@@ -445,25 +563,27 @@ def bench_legged(args, dev, sweeps_list=(4, 8, 16)):
             "flops_per_env_step": flops,
             "roofline": {"bound": "valu", "achieved": achieved_tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": achieved_tf / FP32_PEAK_TFLOPS,
-                         "frac_of_unpacked_peak": achieved_tf / FP32_UNPACKED_TFLOPS, "traffic": None},
+                         "frac_of_unpacked_peak": achieved_tf / FP32_UNPACKED_TFLOPS,
+                         "traffic": LEGGED_ROLLOUT_TRAFFIC.get((c, s))},
             "weight_bytes_per_env_step": 4 * d,
             "weight_stream_gbs": taken * 4 * d / ev / 1e9,
             "fitness_mean": fit_mean,
             "alive_after_steps": {str(t): n for t, n in alive.items()},
         }
         out["by_sweeps"][str(s)] = rec
-        log(f"legged4 ES rollout N={p} H={hidden} S={s} (chunked): {rec['env_steps_per_s']:,.0f} env-steps/s "
+        log(f"legged{c} ES rollout N={p} H={hidden} S={s} (chunked): {rec['env_steps_per_s']:,.0f} env-steps/s "
             f"(mean episode {taken / p:.1f} steps, {ev * 1e3:.1f} ms), {achieved_tf:.2f} TFLOP/s algorithmic, "
             f"weights read at {rec['weight_stream_gbs']:.0f} GB/s")
         log(f"  alive after t steps: {', '.join(f'{t}: {n:,}' for t, n in alive.items() if t in ALIVE_AT)}; "
             f"member-steps in the first 32 steps: {alive['steps_in_first_32']:,}")
-    wall, ev, taken, _ = time_rollout(state, theta, hidden, horizon, c, 8, "rows", 1)
-    out["static_rows_s8_env_steps_per_s"] = taken / wall
-    del theta
-    wall, ev, taken, _ = time_rollout(state, theta_cols, hidden, horizon, c, 8, "columns", 1)
-    out["static_columns_s8_env_steps_per_s"] = taken / wall
-    log(f"legged4 one member per lane, S=8: rows {out['static_rows_s8_env_steps_per_s']:,.0f}, "
-        f"columns {out['static_columns_s8_env_steps_per_s']:,.0f} env-steps/s")
+    if c == 4:
+        wall, ev, taken, _ = time_rollout(state, theta, hidden, horizon, c, 8, "rows", 1)
+        out["static_rows_s8_env_steps_per_s"] = taken / wall
+        del theta
+        wall, ev, taken, _ = time_rollout(state, theta_cols, hidden, horizon, c, 8, "columns", 1)
+        out["static_columns_s8_env_steps_per_s"] = taken / wall
+        log(f"legged4 one member per lane, S=8: rows {out['static_rows_s8_env_steps_per_s']:,.0f}, "
+            f"columns {out['static_columns_s8_env_steps_per_s']:,.0f} env-steps/s")
     del theta_cols
     return out
 
@@ -654,6 +774,18 @@ def bench_es_evaluate(dev, repeats):
     return out
 
 
+def es_flops_per_step(task, hidden):
+    """Algorithmic FP32 operations per step taken of the config-2 fused rollouts, counted from
+    the kernel source as legged_flops_per_step counts (add, sub, mul, div = 1; selects,
+    compares, floor and sign flips not counted; tanh, sin and cos counted separately).
+    CartPole: per hidden unit 4 mul + 4 add and two heads' mul + add (12 H); physics 26
+    (temp 5, angular acceleration 9, cart acceleration 4, Euler 8); plus H tanh and one
+    sin/cos pair. Acrobot: per hidden unit 6 mul + 6 add and three heads' mul + add (18 H);
+    RK4 of four derivative evaluations of 35 each, three stage inputs of 8, the combination
+    28, two wraps of 4, and the termination's 2 (202); plus H tanh and 22 sin/cos."""
+    return 12 * hidden + 26 if task == "cartpole" else 18 * hidden + 202
+
+
 def bench_es_config2(dev, repeats):
     import torch
 
@@ -678,9 +810,14 @@ def bench_es_config2(dev, repeats):
             walls.append(time.perf_counter() - t0)
         wall = statistics.median(walls)
         taken = float(torch.clamp(survived + 1, max=horizon).sum().item())
+        flops = es_flops_per_step(name, hidden)
+        achieved_tf = taken * flops / wall / 1e12
         out[name] = {"P": p, "hidden": hidden, "horizon": horizon, "rollout_s": wall,
                      "steps_taken_per_s": taken / wall, "p_x_horizon_per_s": p * horizon / wall,
-                     "mean_steps_survived": float(survived.mean().item())}
+                     "mean_steps_survived": float(survived.mean().item()), "flops_per_step_taken": flops,
+                     "roofline": {"bound": "valu", "achieved": achieved_tf, "peak": FP32_PEAK_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": achieved_tf / FP32_PEAK_TFLOPS,
+                                  "frac_of_unpacked_peak": achieved_tf / FP32_UNPACKED_TFLOPS, "traffic": None}}
         log(f"ES {name} P={p} H={hidden}: {taken / wall:,.0f} steps-taken/s, {p * horizon / wall:,.0f} PxH/s "
             f"({wall * 1e3:.2f} ms per rollout)")
     return out
@@ -714,7 +851,7 @@ def bench_aba(dev, steps=1000, n=65536, ks=(4, 16, 64)):
         out[str(k)] = {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
                        "bytes_per_env_step": bytes_step,
                        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                    "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
+                                    "frac": achieved / HBM_PEAK_GBS, "traffic": ABA_TRAFFIC.get(k)}}
         log(f"ABA Euler K={k} N={n}: {n * steps / wall:,.0f} env-steps/s, {launch * 1e6:.2f} us per launch, "
             f"{achieved:.0f} GB/s algorithmic")
         del g, bufs
@@ -732,7 +869,9 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
     out = {}
     cases = [(f"pendulum_k{k}", 2 * k, 16 * k + 9, k, n) for k in ks] + [("hopper", 8, 73, "hopper", n),
                                                                          ("acrobot", 4, 41, "acrobot", 262144),
-                                                                         ("legged4_s8", 14, 121, "legged", n)]
+                                                                         ("legged4_s8", 14, 121, "legged", n),
+                                                                         ("legged4_s8_reference", 14, 233,
+                                                                          "legged_ref", n)]
     for name, rows, bytes_step, k, n in cases:
         if k == "hopper":
             bufs = [hopper.Hopper().reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
@@ -749,6 +888,14 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
             fn = _lib.lib().hipenvs_legged_step
             call = lambda t, s, a: fn(4, 8, 0.0, P(bufs[t % 2]), P(a), t + 1, P(stand), P(bufs[(t + 1) % 2]), P(reward),
                                       P(done), n, s)
+        elif k == "legged_ref":
+            # the reference's precision: float64 state in and out (legged_np's dtype after its first step)
+            body = legged.Legged(4, 8)
+            bufs = [body.reset(n, seed=0, device=dev).double(), torch.empty((rows, n), dtype=torch.float64, device=dev)]
+            stand = body.stand_on(dev)
+            fn = _lib.lib().hipenvs_legged_step_reference
+            call = lambda t, s, a: fn(4, 8, 0.0, P(bufs[t % 2]), 1, P(a), t + 1, P(stand), P(bufs[(t + 1) % 2]),
+                                      P(reward), P(done), n, s)
         else:
             bufs = [pendulum.Pendulum(k).reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
             fn = _lib.lib().hipenvs_pendulum_step
@@ -757,7 +904,7 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
         reward = torch.empty(n, device=dev)
         done = torch.empty(n, dtype=torch.bool, device=dev)
         actions = torch.empty((steps, n), dtype=torch.int32, device=dev)
-        n_actions = 81 if k == "legged" else 3
+        n_actions = 81 if k in ("legged", "legged_ref") else 3
         for t in range(steps):
             cartpole.sample_actions(n, m=n_actions, seed=1 + t, device=dev, out=actions[t])
 
@@ -801,28 +948,36 @@ def main():
         torch.cuda.synchronize()
         log(f"calibration copy: {args.copy_mib} MiB x 3")
         del src, dst
-    value = wall = launch = achieved = None
+    head = None
     if args.only in (None, "cartpole"):
-        value, wall, launch, achieved, fused = bench_cartpole(args, dev)
-        extra["cartpole_fused_k32"] = fused
-        extra["cartpole_step_us_per_launch"] = launch * 1e6
+        head = bench_cartpole(args, dev)
+        extra["cartpole_step_kernel_only"] = head["kernel_only"]
+        extra["cartpole_fused_k32"] = head["fused"]
+        extra["cartpole_module_api"] = module_api_rate(args.n, min(args.steps, 1000), dev)
         if args.n != 1 << 20:
             extra["cartpole_step_n1048576"] = bench_cartpole_at(1 << 20, args.steps, args.repeats, dev)
+        extra["cartpole_step_n16777216"] = bench_cartpole_at(1 << 24, 64, args.repeats, dev)
         extra["cartpole_copy_floor"] = [copy_floor(m, args.steps, args.repeats, dev) for m in (args.n, 1 << 20)]
         if args.sweep:
             extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out,
                                             0.0 if args.skip_cpu else 0.25)
     if args.only in (None, "legged"):
-        legged = bench_legged(args, dev)
-        if not args.skip_cpu:
-            rate, csteps = cpu_baseline_legged(args.legged_n, args.legged_cpu_seconds)
-            legged["cpu_baseline"] = {
-                "value": rate, "unit": "env-steps/s", "cores": 1, "kind": "port",
-                "sample": f"numpy ES step (einsum policy + legged step in the reference's literal arithmetic), "
-                          f"N={args.legged_n}, C=4, H=64, S=8, {csteps} timed steps after 1 warm-up"}
-            legged["speedup_vs_cpu_s8"] = legged["by_sweeps"]["8"]["env_steps_per_s"] / rate
-            log(f"legged numpy baseline: {rate:,.0f} env-steps/s -> GPU/CPU {legged['speedup_vs_cpu_s8']:,.0f}x")
-        extra["legged4_es_rollout"] = legged
+        for c in (4, 2):
+            legged = bench_legged(args, dev, c)
+            if not args.skip_cpu:
+                rate, csteps = cpu_baseline_legged(args.legged_n, args.legged_cpu_seconds, c=c)
+                legged["cpu_baseline"] = {
+                    "value": rate, "unit": "env-steps/s", "cores": 1, "kind": "port",
+                    "sample": f"numpy ES step (einsum policy + legged step in the reference's literal arithmetic), "
+                              f"N={args.legged_n}, C={c}, H=64, S=8, {csteps} timed steps after 1 warm-up"}
+                legged["speedup_vs_cpu_s8"] = legged["by_sweeps"]["8"]["env_steps_per_s"] / rate
+                log(f"legged{c} numpy baseline: {rate:,.0f} env-steps/s -> GPU/CPU "
+                    f"{legged['speedup_vs_cpu_s8']:,.0f}x")
+            extra[f"legged{c}_es_rollout"] = legged
+    if args.only == "aba":
+        extra["aba_euler"] = bench_aba(dev)
+        print(json.dumps({"aba_euler": extra["aba_euler"]}), flush=True)
+        return
     if args.only is None:
         extra["es_config2"] = bench_es_config2(dev, args.repeats)
         if not args.skip_cpu:
@@ -856,7 +1011,7 @@ def main():
                          f"single process on a host with os.cpu_count()={os.cpu_count()}"}
         log(f"cartpole numpy baseline: {rate:,.0f} env-steps/s over {csteps} steps")
 
-    if value is None:  # --only legged: the legged rollout is the line
+    if head is None:  # --only legged: the legged rollout is the line
         rec = extra["legged4_es_rollout"]["by_sweeps"]["8"]
         value, wall = rec["env_steps_per_s"], rec["wall_s"]
         roofline = rec["roofline"]
@@ -866,11 +1021,14 @@ def main():
         ms = wall * 1e3
         steps = args.legged_horizon
     else:
-        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": achieved / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(args.n)}
-        config = {"workload": f"cartpole_step, N={args.n}, {args.steps} steps, one launch per step (HIP graph replay)",
-                  "n_envs": args.n, "parallelism": "single GPU, one thread per env"}
-        ms = wall * 1e3 / args.steps
+        value = head["value"]
+        roofline = cartpole_roofline(args.n, head["kernel_only"])
+        config = {"workload": f"cartpole: device action sampler + cartpole_step per iteration, N={args.n}, "
+                              f"{args.steps} iterations per HIP graph, {head['per_region']} graph replays per timed "
+                              f"region, every reward and done row kept",
+                  "n_envs": args.n, "repeats_per_region": head["per_region"], "timed_regions": args.repeats,
+                  "parallelism": "single GPU, one thread per env"}
+        ms = head["wall"] * 1e3 / head["iterations"]
         steps = args.steps
     line = {
         "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
