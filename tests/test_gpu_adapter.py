@@ -1,29 +1,51 @@
-"""The learner-facing DeviceEnv (ppo.MLXEnv's shape) over the step bodies (GPU): the same
-trajectory as calling the body directly."""
+"""The learner-facing DeviceEnv (ppo.MLXEnv's shape) over the step bodies (GPU): trajectories
+of counter-RNG actions checked bit for bit against the oracle's env steps, resets included."""
 
+import numpy as np
 import pytest
 import torch
 
+from oracle import acrobot as oac
+from oracle import cartpole as ocp
+from oracle import hopper as ohp
+from oracle import legged as olg
+from oracle import pendulum as opd
+from oracle import rng
+
 pytestmark = pytest.mark.gpu
 
+# name -> (hipenvs body factory, oracle step(state, action, seed), number of actions)
+BODIES = {
+    "cartpole": (lambda m: m.cartpole, lambda s, a, sd: ocp.step(s, a, sd), 2),
+    "acrobot": (lambda m: m.acrobot, lambda s, a, sd: oac.step(s, a, sd), 3),
+    "hopper": (lambda m: m.hopper.Hopper(), lambda s, a, sd: ohp.Hopper().step(s, a, sd), 3),
+    "legged2": (lambda m: m.legged.Legged(2), lambda s, a, sd: olg.Legged(2).step(s, a, sd), 9),
+    "pendulum4": (lambda m: m.pendulum.Pendulum(4), lambda s, a, sd: opd.Pendulum(4).step(s, a, sd), 3),
+}
 
-@pytest.mark.parametrize("name", ["cartpole", "acrobot", "hopper", "legged2", "pendulum4"])
-def test_device_env_follows_the_body(dev, name):
-    from hipenvs import acrobot, adapter, cartpole, hopper, legged, pendulum
 
-    make = {"cartpole": lambda: cartpole, "acrobot": lambda: acrobot, "hopper": hopper.Hopper,
-            "legged2": lambda: legged.Legged(2), "pendulum4": lambda: pendulum.Pendulum(4)}[name]
-    n_actions = {"cartpole": 2, "acrobot": 3, "hopper": 3, "legged2": 9, "pendulum4": 3}[name]
-    body_a, body_b = make(), make()  # the same module object for module bodies: reseed before each step
-    env = adapter.DeviceEnv(body_a, 300, seed=9, device=dev)
-    state = body_b.reset(300, seed=9, device=dev)
-    assert env.obs().shape == (300, state.shape[0])
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    for t in range(20):
-        a = torch.randint(0, n_actions, (300,), generator=g, device=dev, dtype=torch.int32)
-        body_a.reseed(100 + t)
-        reward, done = env.step(a)
-        body_b.reseed(100 + t)
-        state, r2, d2 = body_b.step(state, a)
-        assert torch.equal(env.state, state) and torch.equal(reward, r2) and torch.equal(done, d2)
+@pytest.mark.parametrize("name", sorted(BODIES))
+def test_device_env_matches_the_oracle(dev, name):
+    """40 steps of uniform counter-RNG actions from the env's own reset: the adapter's state,
+    rewards and done flags equal the oracle's env step at every step (the step counter the
+    body pre-increments is the oracle's seed)."""
+    import hipenvs
+    from hipenvs import acrobot, adapter, cartpole, hopper, legged, pendulum  # noqa: F401 (attributes of hipenvs)
+
+    make, oracle_step, n_actions = BODIES[name]
+    n = 300
+    body = make(hipenvs)
+    env = adapter.DeviceEnv(body, n, seed=9, device=dev)
+    state = env.state.cpu().numpy()
+    assert env.obs().shape == (n, state.shape[0])
+    body.reseed(100)
+    resets = 0
+    for t in range(101, 141):
+        a = rng.uniform_actions(t, n, n_actions)
+        reward, done = env.step(torch.from_numpy(a).to(dev))
+        state, er, ed = oracle_step(state, a, t)
+        np.testing.assert_array_equal(env.state.cpu().numpy(), state, err_msg=f"{name} step {t}")
+        np.testing.assert_array_equal(reward.cpu().numpy(), er, err_msg=f"{name} step {t}")
+        np.testing.assert_array_equal(done.cpu().numpy(), ed, err_msg=f"{name} step {t}")
+        resets += int(ed.sum())
+    assert resets > 0 or name == "pendulum4"

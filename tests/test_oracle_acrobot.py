@@ -69,11 +69,13 @@ def test_matches_gym_scalar_reference(trig):
 
 
 def test_det_trig_close_to_numpy_trig():
+    """One RK4 step with the kernels' sin/cos against numpy's on 50,000 states: measured max
+    4.77e-7 absolute (a few float32 ulps of the velocities), 99.9th percentile 2.4e-7."""
     state, action = random_batch(50_000, seed=4)
     a, b = env.physics(state, action, "det"), env.physics(state, action, "numpy")
     d = np.abs(a - b)
     d[:2] = np.minimum(d[:2], np.abs(d[:2] - 2 * np.pi))
-    assert np.percentile(d, 99.9) < 1e-5 and d.max() < 1e-3
+    assert np.percentile(d, 99.9) <= 3e-7 and d.max() <= 6e-7, (np.percentile(d, 99.9), d.max())
 
 
 def test_terminated_envs_reset_in_place_others_untouched():

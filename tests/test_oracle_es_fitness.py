@@ -1,0 +1,69 @@
+"""ES fitness of the kernels' arithmetic against the reference's own arithmetic (CPU, oracle
+only). The HIP rollouts equal the oracle's fused restatements bit for bit (GPU tests); these
+tests bound how far those restatements sit from the reference's numpy loop, member by member,
+with the reference's own gate (test_es.py:60-69: fitness within rel 1e-3 + abs 1e-2 and equal
+step counts for more than 95 % of members) and the measured agreement.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import acrobot, cartpole, es
+from oracle import legged as olg
+
+
+def config2_population(obs_dim, n_out, p=4096, hidden=32, sigma=0.1, seed=0):
+    """theta0 = 0.1 N(0, 1) and sigma-antithetic pairs around it (es.py:218-222, es.py:340)."""
+    r = np.random.default_rng(seed)
+    d = es.n_params(hidden, obs_dim, n_out)
+    theta0 = (r.standard_normal(d) * 0.1).astype(np.float32)
+    half = r.standard_normal((p // 2, d)).astype(np.float32)
+    return (theta0[None, :] + np.float32(sigma) * np.concatenate([half, -half])).astype(np.float32)
+
+
+@pytest.mark.parametrize("name", ["cartpole", "acrobot"])
+def test_config2_fitness_under_the_reference_trig(name):
+    """The config-2 rollout (P = 4,096, H = 32, sigma 0.1, horizon 500) with the kernels'
+    deterministic sin/cos/tanh against the same rollout with numpy's np.sin/np.cos/np.tanh, the
+    reference's: measured 100 % of members identical for CartPole and 99.4 % for Acrobot
+    (its chaotic swing-up lets a 1-ulp difference change when the tip clears the line)."""
+    env, obs_dim, n_out, fn = ((cartpole, 4, 2, cartpole.rollout_survived) if name == "cartpole" else
+                               (acrobot, 6, 3, acrobot.rollout_steps))
+    pop = config2_population(obs_dim, n_out)
+    state = env.reset(pop.shape[0], seed=0)
+    det = fn(state, pop, 32, 500, trig="det")
+    ref = fn(state, pop, 32, 500, trig="numpy")
+    same = (det == ref).mean()
+    assert same > 0.95                                        # the reference's gate
+    assert same >= (1.0 if name == "cartpole" else 0.99), same  # measured
+
+
+@pytest.mark.parametrize("c,measured_close", [(2, 1.0), (4, 0.98)])
+def test_legged_fused_float32_against_the_reference_loop(c, measured_close):
+    """The fused float32 legged rollout (the HIP kernels' arithmetic: float32 physics,
+    deterministic trig, bias-first policy sums) against the reference's numpy loop: es.py's
+    loop_fitness over legged_np.Legged.step with its float64 promotion, np.tanh and the einsum
+    policy (es.py:167-193), at the config-4 population (H = 64, sigma 0.03 around
+    0.1 N(0, 1)), P = 256, horizon 200, 8 sweeps. Measured: C = 2 every member within the
+    tolerance with equal steps (max fitness difference 7e-5); C = 4 98.4 % within it and
+    99.2 % equal steps."""
+    p, hidden, horizon = 256, 64, 200
+    r = np.random.default_rng(c)
+    d = es.n_params(hidden, 5 + 2 * c, 3 * c)
+    theta0 = (r.standard_normal(d) * 0.1).astype(np.float32)
+    half = r.standard_normal((p // 2, d)).astype(np.float32)
+    pop = (theta0[None, :] + np.float32(0.03) * np.concatenate([half, -half])).astype(np.float32)
+    state = olg.Legged(c).reset(p, seed=3)
+    fit_k, steps_k = olg.rollout_fused(state, pop, hidden, horizon, c)
+    w1, b1, w2, b2 = es.unflatten(pop, hidden, 5 + 2 * c, 3 * c)
+    body = olg.Legged(c, 8, mode="reference", trig="numpy")
+
+    def logits(st):
+        h = np.tanh(np.einsum("pi,pih->ph", st[1:].T, w1) + b1)
+        return np.einsum("ph,pho->po", h, w2) + b2
+
+    fit_l, steps_l = es.loop_fitness(body.step, logits, lambda lg: es.legged_action(lg, c), state, (), horizon,
+                                     seed0=1)
+    close = np.abs(fit_k - fit_l) <= 1e-3 * np.maximum(np.abs(fit_l), 1.0) + 1e-2
+    assert close.mean() > 0.95 and (steps_k == steps_l).mean() > 0.95   # the reference's gate
+    assert close.mean() >= measured_close and (steps_k == steps_l).mean() >= measured_close
