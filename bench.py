@@ -46,7 +46,8 @@ sample of about `--cpu-seconds` seconds on this host.
   reference's numpy ES loop (all members stepped every iteration) timed beside them in
   member-steps/s, to compare with the GPU's P x horizon rate;
 * `aba_euler`: the K-link pendulum, semi-implicit Euler dt 0.01, N = 65,536,
-  K = 4/16/64, 1,000 graph-replayed steps, with its HBM roofline (16K + 9 B) and the
+  K = 4/16/64, 1,000 graph-replayed steps with the U[-1, 1] root torque drawn in the
+  kernel, with its HBM roofline (16K + 5 B: state in and out, reward, done) and the
   numpy ABA Euler step timed beside it;
 * `es_generation`: one whole ES generation (noise, rollout, centered ranks,
   update) two ways: "materialised" is the reference's generation (es.py:218-227)
@@ -88,23 +89,19 @@ HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3           # MI355X FP32 vector, packed (published)
 FP32_UNPACKED_TFLOPS = 78.6        # one FMA per lane per cycle
 CARTPOLE_BYTES = 41
-# HBM bytes per cartpole_step launch: rocprofv3 --pmc FETCH_SIZE and then WRITE_SIZE over
-# `bench.py --only cartpole --copy-mib 256` read 2580.5 / 5377.2 KiB per dispatch at N = 2**18
-# and 10260.5 / 21649.5 KiB at N = 2**20; the same counters read 131085.2 and 262144.0 KiB
-# for the 256 MiB device copy in the same process, so they are scaled by 2.000 and 1.000.
-# Commands and tables: profiles/cartpole_step_n262144.md. Algorithmic bytes: 41 x N.
-_FETCH_SCALE = 262144.0 / 131085.2
-CARTPOLE_TRAFFIC = {n: int(round((fetch * _FETCH_SCALE + write) * 1024))
-                    for n, fetch, write in ((1 << 18, 2580.5, 5377.2), (1 << 20, 10260.5, 21649.5))}
-
-
-# HBM bytes per launch of the ABA Euler step at N = 65,536 and per rollout of the legged ES
-# rollout at N = 262,144 (all of its chunk and tail kernels), keyed by K and by (C, S):
-# FETCH_SIZE + WRITE_SIZE from rocprofv3 --pmc runs of `bench.py --only legged` / the ABA
-# block, scaled like CARTPOLE_TRAFFIC; profiles/aba_euler_n65536.md and
-# profiles/legged_es_rollout_n262144.md hold the tables. None where not collected.
-ABA_TRAFFIC = {}
-LEGGED_ROLLOUT_TRAFFIC = {}
+# HBM bytes per launch: rocprofv3 --pmc FETCH_SIZE and then WRITE_SIZE (one counter per run)
+# over `bench.py --only cartpole --skip-cpu --steps 32 --warmup 2 --repeats 1 --region-seconds
+# 0.0001 --copy-mib 256`, `bench.py --only aba --skip-cpu --copy-mib 256` and `bench.py --only
+# legged --skip-cpu --repeats 1 --copy-mib 256`, in KiB per dispatch. The same counters read
+# 131085.3 and 262144.0 KiB for the 256 MiB device copy in the same process, so FETCH_SIZE is
+# scaled by 2.000 and WRITE_SIZE by 1.000. Algorithmic bytes: 41 x N for the CartPole step.
+# Tables and commands: profiles/cartpole_step_n262144.md, profiles/aba_euler_n65536.md,
+# profiles/legged_es_rollout_n262144.md.
+CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
+ABA_TRAFFIC = {4: 4654910, 16: 17652928, 64: 119529808}
+# per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 176430000000, (4, 8): 185150000000, (4, 16): 210200000000,
+                          (2, 4): 152290000000, (2, 8): 155070000000, (2, 16): 144780000000}
 
 
 def log(msg):
@@ -339,7 +336,7 @@ def module_api_rate(n, steps, dev):
 # default command (`bench.py`, all of whose step launches at a given N are traced), in ns;
 # profiles/cartpole_step_n262144.md tabulates them. The tracer runs each dispatch on its own,
 # so these include the per-dispatch ramp and drain that back-to-back launches overlap.
-CARTPOLE_TRACE_NS = {1 << 18: 3349.0, 1 << 20: 8159.0}
+CARTPOLE_TRACE_NS = {1 << 18: 3561.5, 1 << 20: 8518.8, 1 << 24: 110860.0}
 
 
 def cartpole_roofline(n, kernel_only):
@@ -398,8 +395,7 @@ def bench_cartpole_at(n, steps, repeats, dev):
     log(f"cartpole_step N={n}: {n * steps / wall:,.0f} env-steps/s; {launch * 1e6:.3f} us per launch -> {gbs:.1f} GB/s")
     del run
     return {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
-            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gbs / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(n)}}
+            "roofline": cartpole_roofline(n, {"us_per_launch_events": launch * 1e6, "achieved_gbs_events": gbs})}
 
 
 def cpu_baseline_cartpole(n, seconds):
@@ -846,7 +842,7 @@ def bench_aba(dev, steps=1000, n=65536, ks=(4, 16, 64)):
         g = capture_graph(dev, body)
         wall, ev = time_replay(g, 3)
         launch = ev / steps
-        bytes_step = 16 * k + 9
+        bytes_step = 16 * k + 5  # 2K floats in and out, reward, done; the torque is drawn in the kernel
         achieved = bytes_step * n / launch / 1e9
         out[str(k)] = {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
                        "bytes_per_env_step": bytes_step,

@@ -243,7 +243,10 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
 template <int H>
 int launch_rollout(const float* state, const float* theta, int64_t member_stride, int64_t p, int32_t horizon,
                    float* out, hipStream_t s) {
-  if (p <= group_rollout_limit()) {
+  int64_t limit = 0;
+  const int status = group_rollout_limit(&limit);
+  if (status != HIPENVS_OK) return status;
+  if (p <= limit) {
     hipLaunchKernelGGL(rollout_group_kernel<H>, dim3((unsigned)((p + kRolloutMembers - 1) / kRolloutMembers)),
                        dim3(64), 0, s, state, theta, member_stride, p, horizon, out);
   } else {

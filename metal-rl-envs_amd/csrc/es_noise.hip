@@ -155,19 +155,15 @@ int launch_update(const float* theta, const float* ranks, int64_t d, int64_t p, 
 constexpr int64_t kStaticPartialFloats = HIPENVS_ES_UPDATE_STATIC_BYTES / (int64_t)sizeof(float);
 __device__ __align__(256) float scratch[kStaticPartialFloats];
 
-constexpr int kMaxDevices = 64;
 std::atomic<float*> g_scratch[kMaxDevices];
 std::mutex g_scratch_mutex;
 
 // The current device's address of `scratch`, or a negative status.
 int static_partials(float** out) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) {
-    set_last_hip_error((int)e);
-    return HIPENVS_E_HIP;
-  }
-  if (dev < 0 || dev >= kMaxDevices) return HIPENVS_E_ARG;
+  const int status = current_device(&dev);
+  if (status != HIPENVS_OK) return status;
+  hipError_t e = hipSuccess;
   float* ptr = g_scratch[dev].load(std::memory_order_acquire);
   if (!ptr) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);

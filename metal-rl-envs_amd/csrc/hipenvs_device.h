@@ -7,6 +7,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/hipenvs.h"
 
 namespace hipenvs {
@@ -270,21 +273,57 @@ __device__ __forceinline__ float clip(float v, float lo, float hi) {
 // ---------------------------------------------------------------------------
 constexpr int kBlock = 256;
 
+void set_last_hip_error(int err);
+
+constexpr int kMaxDevices = 64;
+
+// The current device's index into per-device caches; HIPENVS_E_HIP (error recorded) when
+// hipGetDevice fails, HIPENVS_E_ARG past kMaxDevices devices.
+int current_device(int* dev);
+
+// Compute units of the current device, queried once per device (the answer cannot change
+// while the process runs); a negative status when the query fails.
+int device_cus(int* cus);
+
 // Populations up to this size run the fused ES rollouts with a lane group per member: 16
-// members per CU, i.e. one four-member wave per SIMD. 0 when the device cannot be queried.
-inline int64_t group_rollout_limit() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                               hipSuccess)
-    return 0;
-  return 16 * (int64_t)cus;
+// members per CU, i.e. one four-member wave per SIMD.
+inline int group_rollout_limit(int64_t* limit) {
+  int cus = 0;
+  const int status = device_cus(&cus);
+  *limit = 16 * (int64_t)cus;
+  return status;
+}
+
+// Resident 64-thread workgroups per CU of `kernel` on the current device, queried once per
+// device for each kernel (Tag distinguishes the callers' caches); a negative status on failure.
+template <class Tag, class Kernel>
+int resident_blocks_per_cu(Kernel kernel, int* per_cu) {
+  static int cache[kMaxDevices];  // 0: not yet queried; written once per device under the lock below
+  static std::atomic<int> ready[kMaxDevices];
+  static std::mutex lock;
+  int dev = 0;
+  const int status = current_device(&dev);
+  if (status != 0) return status;
+  if (!ready[dev].load(std::memory_order_acquire)) {
+    std::lock_guard<std::mutex> guard(lock);
+    if (!ready[dev].load(std::memory_order_relaxed)) {
+      int blocks = 0;
+      const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64, 0);
+      if (e != hipSuccess) {
+        set_last_hip_error((int)e);
+        return -3;  // HIPENVS_E_HIP
+      }
+      cache[dev] = blocks > 0 ? blocks : 1;
+      ready[dev].store(1, std::memory_order_release);
+    }
+  }
+  *per_cu = cache[dev];
+  return 0;
 }
 
 inline unsigned grid_for(int64_t items, int block = kBlock) {
   return (unsigned)((items + block - 1) / block);
 }
-
-void set_last_hip_error(int err);
 
 // Checks the launch just enqueued; returns HIPENVS_OK or HIPENVS_E_HIP.
 inline int launch_status() {

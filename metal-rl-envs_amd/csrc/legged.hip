@@ -1157,6 +1157,10 @@ int launch_later_chunk(const float* state0, const float* theta0, int64_t p, cons
   return launch_status();
 }
 
+// Tag of the per-device occupancy cache of rollout_chunk_kernel<C, HID, false>.
+template <int C, int HID>
+struct ChunkTag {};
+
 template <int C, int HID>
 int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32_t horizon, int iters,
                    int32_t chunk_steps, float alive, float fall, float gate, double assist, float* fitness,
@@ -1179,12 +1183,11 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   }
   set[0].count = reinterpret_cast<uint32_t*>(ws);
   set[1].count = set[0].count + 1;
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rollout_chunk_kernel<C, HID, false>, 64, 0) !=
-          hipSuccess)
-    return launch_status();
+  int cus = 0, per_cu = 0;
+  int query = device_cus(&cus);
+  if (query == HIPENVS_OK)
+    query = resident_blocks_per_cu<ChunkTag<C, HID>>(rollout_chunk_kernel<C, HID, false>, &per_cu);
+  if (query != HIPENVS_OK) return query;
   const int64_t needed = (p + 63) / 64;
   int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
   const float af = (float)assist, ad = (float)(0.1 * assist);
@@ -1229,12 +1232,11 @@ int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uin
   }
   set[0].count = reinterpret_cast<uint32_t*>(ws);
   set[1].count = set[0].count + 1;
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rollout_chunk_kernel<C, HID, false>, 64, 0) !=
-          hipSuccess)
-    return launch_status();
+  int cus = 0, per_cu = 0;
+  int query = device_cus(&cus);
+  if (query == HIPENVS_OK)
+    query = resident_blocks_per_cu<ChunkTag<C, HID>>(rollout_chunk_kernel<C, HID, false>, &per_cu);
+  if (query != HIPENVS_OK) return query;
   const int64_t needed = (p + 63) / 64;
   const int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
   const int64_t grid = resident < needed ? resident : needed;
