@@ -48,4 +48,6 @@ def test_device_env_matches_the_oracle(dev, name):
         np.testing.assert_array_equal(reward.cpu().numpy(), er, err_msg=f"{name} step {t}")
         np.testing.assert_array_equal(done.cpu().numpy(), ed, err_msg=f"{name} step {t}")
         resets += int(ed.sum())
-    assert resets > 0 or name == "pendulum4"
+    # random actions end CartPole, hopper and biped episodes within 40 steps; the swinging
+    # chains (Acrobot, pendulum) almost never terminate that early
+    assert resets > 0 or name in ("acrobot", "pendulum4")
