@@ -170,10 +170,12 @@ __device__ __forceinline__ void det_sincos_near_zero(float x, float* sin_out, fl
 }
 
 // Lane L's value of each 16-lane row of the wave, on every lane of that row (DPP
-// row_newbcast:L): how a 16-lane group shares a value one of its lanes computed.
+// row_newbcast:L): how a 16-lane group shares a value one of its lanes computed. Every lane
+// of every row is written, so the destination needs no prior value (mov_dpp, not update_dpp
+// with an initialised old value, which costs a v_mov per broadcast).
 template <int L>
 __device__ __forceinline__ float group_bcast(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xF, 0xF, false));
 }
 
 __device__ __forceinline__ float det_sin(float x) {

@@ -17,6 +17,8 @@
 // (P, D) or from a column layout (D, P) in which a wave's 64 members read 256
 // contiguous bytes per weight.
 
+#include <type_traits>
+
 #include "es_noise.h"
 
 namespace hipenvs {
@@ -365,23 +367,97 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       blk[k] = contact_block(Att[k][k], Atn[k][k], Ann[k][k]);
     }
   }
-  for (int it = 0; it < iters; ++it) {
+  if constexpr (kGroup == 16) {
+    // The member's 16 lanes split each contact's independent work and share the results by
+    // row broadcast: lane 1 forms the normal coupling sum and every other lane the tangential
+    // one (each with its own coefficient rows), and lanes 0-3 form the four quotients of the
+    // contact solve, ln_stick, lt_stick, (target - wn) / den_p and (target - wn) / den_m
+    // (lanes 4-15 repeat lane 0's). Every broadcast value is the expression the one-lane
+    // sweep evaluates, so the impulses are the same bits.
+    const bool nrow = (g == 1);
+    float cA[C][C], cB[C][C], w0x[C], qP[C], qQ[C], qd[C], slipc[C];
+    double qr[C];
 #pragma unroll
     for (int k = 0; k < C; ++k) {
-      float st = 0.0f, sn = 0.0f;
-      bool first = true;
 #pragma unroll
       for (int l = 0; l < C; ++l) {
-        if (l == k) continue;
-        const float tt = Att[k][l] * lt[l] + Atn[k][l] * ln[l];
-        const float nn = Ant[k][l] * lt[l] + Ann[k][l] * ln[l];
-        st = first ? tt : st + tt;
-        sn = first ? nn : sn + nn;
-        first = false;
+        cA[k][l] = nrow ? Ant[k][l] : Att[k][l];
+        cB[k][l] = nrow ? Ann[k][l] : Atn[k][l];
       }
-      const float wt = (C == 1) ? w0t[k] : w0t[k] + st;
-      const float wn = (C == 1) ? w0n[k] : w0n[k] + sn;
-      contact_impulse(blk[k], wt, wn, depth[k], lt[k], ln[k], div);
+      w0x[k] = nrow ? w0n[k] : w0t[k];
+      // numerators P * X + Q * Y: lane 0 Att tw + Atn wt; lane 1 (-Ann) wt + (-Atn) tw, which is
+      // the reference's (-Ann) wt - Atn tw exactly (a - b = a + (-b), and the sum commutes)
+      qP[k] = nrow ? -blk[k].Ann : blk[k].Att;
+      qQ[k] = nrow ? -blk[k].Atn : blk[k].Atn;
+      qd[k] = (g == 2) ? blk[k].den_p : (g == 3) ? blk[k].den_m : blk[k].det;
+      qr[k] = (g == 2) ? blk[k].rden_p : (g == 3) ? blk[k].rden_m : blk[k].rdet;
+      slipc[k] = blk[k].Att * MU + blk[k].Atn;
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        float wt, wn;
+        if constexpr (C == 1) {
+          wt = w0t[k];
+          wn = w0n[k];
+        } else {
+          float sx = 0.0f;
+          bool first = true;
+#pragma unroll
+          for (int l = 0; l < C; ++l) {
+            if (l == k) continue;
+            const float tx = cA[k][l] * lt[l] + cB[k][l] * ln[l];
+            sx = first ? tx : sx + tx;
+            first = false;
+          }
+          const float wx = w0x[k] + sx;
+          wt = group_bcast<0>(wx);
+          wn = group_bcast<1>(wx);
+        }
+        const ContactBlock& b = blk[k];
+        const bool touching = depth[k] >= 0.0f;
+        const float target = BAUMGARTE_OVER_H * max0(depth[k]);
+        const float tw = target - wn;
+        const float X = nrow ? wt : tw, Y = nrow ? tw : wt;
+        const float num = (g == 2 || g == 3) ? tw : qP[k] * X + qQ[k] * Y;
+        const float quo = div(num, qd[k], qr[k]);
+        const float ln_stick = group_bcast<0>(quo);
+        const float lt_stick = group_bcast<1>(quo);
+        const float q_p = group_bcast<2>(quo);
+        const float q_m = group_bcast<3>(quo);
+        const bool sticks = fabsf(lt_stick) <= MU * ln_stick;
+        const float ln_p = (b.den_p > 0.0f) ? max0(q_p) : 0.0f;
+        const float ln_m = (b.den_m > 0.0f) ? max0(q_m) : 0.0f;
+        const float slip_p = wt + slipc[k] * ln_p;
+        const float sgn = (slip_p <= 0.0f) ? 1.0f : -1.0f;
+        const float ln_slide = (slip_p <= 0.0f) ? ln_p : ln_m;
+        const float lt_slide = (MU * sgn) * ln_slide;
+        const float lnv = sticks ? ln_stick : ln_slide;
+        const float ltv = sticks ? lt_stick : lt_slide;
+        const bool active = touching && (lnv > 0.0f) && (wn < target);
+        lt[k] = active ? ltv : 0.0f;
+        ln[k] = active ? lnv : 0.0f;
+      }
+    }
+  } else {
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        float st = 0.0f, sn = 0.0f;
+        bool first = true;
+#pragma unroll
+        for (int l = 0; l < C; ++l) {
+          if (l == k) continue;
+          const float tt = Att[k][l] * lt[l] + Atn[k][l] * ln[l];
+          const float nn = Ant[k][l] * lt[l] + Ann[k][l] * ln[l];
+          st = first ? tt : st + tt;
+          sn = first ? nn : sn + nn;
+          first = false;
+        }
+        const float wt = (C == 1) ? w0t[k] : w0t[k] + st;
+        const float wn = (C == 1) ? w0n[k] : w0n[k] + sn;
+        contact_impulse(blk[k], wt, wn, depth[k], lt[k], ln[k], div);
+      }
     }
   }
   // v = v_free + sum_k M^-1 J_k^T lambda_k; q += h v
@@ -732,6 +808,72 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_kernel(c
 // stands, the score adds the evaluation's term (reward - 1) + eval_bonus with the
 // environment's reward v_x + 1 (legged_np.py:118-121); the step that falls adds nothing
 // and ends the episode. All lanes read the same weight at once.
+// A compacted member's policy weights held in the registers of its G-lane group for the
+// rest of its episode (the group tail runs one wave per SIMD, so the registers are there):
+// lane g keeps the bias and input weights of hidden units g, g + G, ... and, for g < 3C, the
+// weights of head g over every hidden unit. policy() then computes policy_group's sums, in
+// the same order, without reading memory; loading the weights from the packed tile once
+// replaces a dependent chain of memory round trips per step (the head sums' loads).
+template <int C, int HID, int G>
+struct ResidentPolicy {
+  static constexpr int OBS = 5 + 2 * C, OUT = 3 * C, U = (HID + G - 1) / G;
+  static_assert(OUT <= G, "one head per lane");
+  float w1[U][OBS], b1[U], w2[HID], b2;
+
+  __device__ __forceinline__ void load(const float* __restrict__ w, int g) {
+    using R = UnitRows<OBS, HID, OUT>;
+    constexpr int64_t kStride = 64;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = g + G * u < HID ? g + G * u : 0;  // lanes past HID hold unit 0, unused
+      b1[u] = w[R::b1(j) * kStride];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) w1[u][k] = w[R::w1(k, j) * kStride];
+    }
+    const int o = g < OUT ? g : 0;  // lanes past the heads hold head 0, unused
+    b2 = w[R::b2(o) * kStride];
+#pragma unroll
+    for (int j = 0; j < HID; ++j) w2[j] = w[R::w2(j, o) * kStride];
+  }
+
+  __device__ __forceinline__ void policy(const float (&q)[3 + C], const float (&v)[3 + C], float (&tq)[C],
+                                         float* xh, float* xl, int g) const {
+    constexpr int N = 3 + C;
+    float obs[OBS];
+#pragma unroll
+    for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
+    float hs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float sj = b1[u];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) sj = sj + obs[k] * w1[u][k];
+      hs[u] = det_tanh(sj);
+    }
+    __syncthreads();  // the rows' previous readers are done
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (g + G * u < HID) xh[g + G * u] = hs[u];
+    __syncthreads();
+    if (g < OUT) {
+      float lo = b2;
+#pragma unroll
+      for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w2[j];
+      xl[g] = lo;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int leg = 0; leg < C; ++leg) {
+      float torque = -1.0f, best = xl[3 * leg];
+      if (xl[3 * leg + 1] > best) { torque = 0.0f; best = xl[3 * leg + 1]; }
+      if (xl[3 * leg + 2] > best) { torque = 1.0f; }
+      tq[leg] = torque * TORQUE;
+    }
+  }
+};
+
 template <int C, int HID>
 __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void evaluate_kernel(const float* __restrict__ state,
                                                                              const float* __restrict__ theta,
@@ -846,9 +988,17 @@ __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& d
     const int32_t id = src.meta[slot];
     int32_t t = src.meta[cap + slot];
     const float* w = src.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
+    // the tail (which runs each member to the end at one wave per SIMD) keeps the member's
+    // weights in registers; a group chunk reads them from its tile every step
+    struct NoResident {};
+    std::conditional_t<kChunk, NoResident, ResidentPolicy<C, HID, G>> resident;
+    if constexpr (!kChunk) resident.load(w, g);
     // every lane steps while any member of the wave is live, so the barriers stay uniform
     for (int32_t k = 0; (!kChunk || k < chunk_steps) && __any(live); ++k) {
-      policy_group<C, HID, G>(w, q, v, tq, xh, xl, g);
+      if constexpr (kChunk)
+        policy_group<C, HID, G>(w, q, v, tq, xh, xl, g);
+      else
+        resident.policy(q, v, tq, xh, xl, g);
 #pragma unroll 1
       for (int sub = 0; sub < SUBSTEPS; ++sub)
         substep_exact_group<C, G>(q, v, tq, iters, assist, assist_damping, xs, g, live, xd);
