@@ -937,7 +937,8 @@ __host__ __device__ constexpr int64_t round_to_tile(int64_t n) { return (n + kTi
 // one-lane schedule, bit for bit.
 constexpr int kGroupLanes = 16;
 #ifndef LEGGED_TAIL_MEMBERS_PER_CU
-#define LEGGED_TAIL_MEMBERS_PER_CU 16  // survivors per CU at the switch: one 4-member wave per SIMD
+// survivors per CU at the switch per tail wave on each SIMD (4-member waves; x kTailWaves<C>)
+#define LEGGED_TAIL_MEMBERS_PER_CU 16
 #endif
 // Above the tail's bound and up to this many survivors per CU, a chunk runs in the group form
 // (rollout_group_chunk_kernel) instead of one member per lane, with LEGGED_GROUP_CHUNK_LANES
@@ -952,6 +953,11 @@ constexpr int kGroupLanes = 16;
 #endif
 constexpr int kChunkGroupLanes = LEGGED_GROUP_CHUNK_LANES;
 constexpr int kGroupMembers = 64 / kGroupLanes;
+// Waves per SIMD the group tail runs at. With its members' weights in registers it needs 235
+// VGPRs at C = 2 (H = 64), so two waves share a SIMD and the tail takes over at twice the
+// survivors per CU; at C = 4 it needs 256 + 66 AGPRs, one wave per SIMD.
+template <int C>
+constexpr int kTailWaves = C <= 2 ? 2 : 1;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
 template <int C>
 constexpr int kBlockFloats = 4 * C * C + 12 * C;
@@ -1064,7 +1070,7 @@ __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& d
 // set holds at most wide_max members and exits at once otherwise (the chunk kernels do the
 // opposite). Kept apart so that the one-lane kernel's code is compiled on its own.
 template <int C, int HID>
-__global__ __launch_bounds__(64) void rollout_tail_kernel(Packed src, int64_t cap, int32_t horizon, int iters,
+__global__ __launch_bounds__(64, kTailWaves<C>) void rollout_tail_kernel(Packed src, int64_t cap, int32_t horizon, int iters,
                                                           float alive_bonus, float fall, float gate, float assist,
                                                           float assist_damping, float* __restrict__ fitness,
                                                           float* __restrict__ steps_out, int64_t wide_max) {
@@ -1273,9 +1279,10 @@ struct GroupBounds {
   int64_t wide_max, group_max, group_grid, tail_grid;
 };
 
+template <int C>
 inline GroupBounds group_bounds(int64_t p, int cus) {
   GroupBounds b;
-  b.wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * cus;
+  b.wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * kTailWaves<C> * cus;
   const int64_t gm = (int64_t)LEGGED_GROUP_CHUNK_MEMBERS_PER_CU * cus;
   b.group_max = gm > b.wide_max ? gm : b.wide_max;
   // one member group per workgroup: a kernel never holds more than min(p, its bound) members
@@ -1343,7 +1350,7 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   const float af = (float)assist, ad = (float)(0.1 * assist);
   // first chunk: the caller's arrays -> set 0
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
-  const GroupBounds gb = group_bounds(p, cus);
+  const GroupBounds gb = group_bounds<C>(p, cus);
   hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true>), dim3((unsigned)needed), dim3(64), 0, s, state, theta_cols,
                      p, set[1], set[0], cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
                      gb.group_max);
@@ -1390,7 +1397,7 @@ int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uin
   const int64_t needed = (p + 63) / 64;
   const int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
   const int64_t grid = resident < needed ? resident : needed;
-  const GroupBounds gb = group_bounds(p, cus);
+  const GroupBounds gb = group_bounds<C>(p, cus);
   const float af = (float)assist, ad = (float)(0.1 * assist);
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, (uint32_t)p);
   hipLaunchKernelGGL((seed_set_kernel<C, HID>), dim3((unsigned)((p / 2 + 63) / 64)), dim3(64), 0, s, state, theta, p,

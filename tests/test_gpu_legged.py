@@ -162,15 +162,16 @@ def test_group_tail_equals_static(dev, c, hidden, iters):
 
 @pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (2, 32, 8), (4, 64, 8), (2, 64, 4), (4, 64, 16)])
 def test_group_chunk_equals_static(dev, c, hidden, iters):
-    """Populations of 24 members per CU: above the group tail's bound (16 per CU) and within
-    the group chunk's (48 per CU), so later chunks run in the group form (8 lanes per member:
-    two solves, two Delassus blocks and up to two heads per lane) and append their survivors
-    until the count falls to the tail's bound: member for member equal to the one-lane
-    kernel."""
+    """Populations above the group tail's bound (16 members per CU at C = 4, 32 at C <= 2,
+    where the tail runs two waves per SIMD) and within the group chunk's (48 per CU), so
+    later chunks run in the group form (8 lanes per member: two solves, two Delassus blocks
+    and up to two heads per lane) and append their survivors until the count falls to the
+    tail's bound: member for member equal to the one-lane kernel."""
     from hipenvs import legged, legged_rollout
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    p, horizon = 24 * cus, 60
+    tail_per_cu = 16 if c == 4 else 32
+    p, horizon = (tail_per_cu + 8) * cus, 60
     state = legged.Legged(c).reset(p, seed=6, device=dev)
     past_first = 0
     for assist, scale in ((0.0, 0.3), (20.0, 0.0)):
@@ -181,7 +182,7 @@ def test_group_chunk_equals_static(dev, c, hidden, iters):
                                         iters=iters)
         assert torch.equal(fq, fs) and torch.equal(sq, ss), (c, hidden, assist)
         past_first = max(past_first, int((ss > 8).sum().item()))
-    assert past_first > 16 * cus  # the second chunk ran in the group form
+    assert past_first > tail_per_cu * cus  # the second chunk ran in the group form
 
 
 def test_shaped_reward_and_assist_match_oracle(dev):
