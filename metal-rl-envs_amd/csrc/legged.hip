@@ -672,12 +672,19 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
   for (int u = 0; u < (HID + G - 1) / G; ++u)
     if (g + G * u < HID) xh[g + G * u] = hs[u];
   __syncthreads();
-  // lane g sums heads g, g + G, ... over the hidden values in order
+  // lane g sums heads g, g + G, ... over the hidden values in order; a head's HID weights are
+  // loaded together (one memory round trip per head), from an opaque copy of the address so
+  // that the loads stay here (not hoisted out of the caller's step loop)
+  const float* wh = w;
+  asm volatile("" : "+v"(wh));
 #pragma unroll
   for (int o = g; o < OUT; o += G) {
+    float w2r[HID];
+#pragma unroll
+    for (int j = 0; j < HID; ++j) w2r[j] = wh[R::w2(j, o) * kStride];
     float lo = w[R::b2(o) * kStride];
-#pragma unroll 8
-    for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w[R::w2(j, o) * kStride];
+#pragma unroll
+    for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w2r[j];
     xl[o] = lo;
   }
   __syncthreads();
@@ -803,13 +810,9 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void rollout_kernel(c
   steps_out[e] = taken;
 }
 
-// The greedy evaluation of one policy (es.py:308-322): every env runs the shared weights
-// theta (D) without assist from its own start state for up to `steps` steps. While the body
-// stands, the score adds the evaluation's term (reward - 1) + eval_bonus with the
-// environment's reward v_x + 1 (legged_np.py:118-121); the step that falls adds nothing
-// and ends the episode. All lanes read the same weight at once.
 // A compacted member's policy weights held in the registers of its G-lane group for the
-// rest of its episode (the group tail runs one wave per SIMD, so the registers are there):
+// rest of its episode (the group tail runs one or two waves per SIMD, so the registers are
+// there):
 // lane g keeps the bias and input weights of hidden units g, g + G, ... and, for g < 3C, the
 // weights of head g over every hidden unit. policy() then computes policy_group's sums, in
 // the same order, without reading memory; loading the weights from the packed tile once
@@ -874,6 +877,11 @@ struct ResidentPolicy {
   }
 };
 
+// The greedy evaluation of one policy (es.py:308-322): every env runs the shared weights
+// theta (D) without assist from its own start state for up to `steps` steps. While the body
+// stands, the score adds the evaluation's term (reward - 1) + eval_bonus with the
+// environment's reward v_x + 1 (legged_np.py:118-121); the step that falls adds nothing
+// and ends the episode. All lanes read the same weight at once.
 template <int C, int HID>
 __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void evaluate_kernel(const float* __restrict__ state,
                                                                              const float* __restrict__ theta,
@@ -953,9 +961,11 @@ constexpr int kGroupLanes = 16;
 #endif
 constexpr int kChunkGroupLanes = LEGGED_GROUP_CHUNK_LANES;
 constexpr int kGroupMembers = 64 / kGroupLanes;
-// Waves per SIMD the group tail runs at. With its members' weights in registers it needs 235
+// Waves per SIMD the group tail runs at. With its members' weights in registers it needs 218
 // VGPRs at C = 2 (H = 64), so two waves share a SIMD and the tail takes over at twice the
-// survivors per CU; at C = 4 it needs 256 + 66 AGPRs, one wave per SIMD.
+// survivors per CU; at C = 4 it needs 256 + 66 AGPRs, one wave per SIMD. (Reloading the
+// weights every step instead fits two waves at C = 4, 206 VGPRs, but the ES rollout at
+// N = 262,144 and 8 sweeps took 60.8 instead of 50.9 ms.)
 template <int C>
 constexpr int kTailWaves = C <= 2 ? 2 : 1;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
