@@ -68,7 +68,7 @@ sample of about `--cpu-seconds` seconds on this host.
   of repeats, and both scores.
 
 Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--repeats 3] [--sweep] [--skip-cpu]
-                      [--only cartpole|legged]
+                      [--only cartpole|legged|aba|steps]
 """
 
 import argparse
@@ -100,8 +100,8 @@ CARTPOLE_BYTES = 41
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
 ABA_TRAFFIC = {4: 4654910, 16: 17652928, 64: 119529808}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 176430000000, (4, 8): 185150000000, (4, 16): 210200000000,
-                          (2, 4): 152290000000, (2, 8): 155070000000, (2, 16): 144780000000}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110160000000, (4, 8): 125670000000, (4, 16): 139980000000,
+                          (2, 4): 58598000000, (2, 8): 64125000000, (2, 16): 89396000000}
 
 
 def log(msg):
@@ -121,9 +121,10 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--legged-cpu-seconds", type=float, default=12.0)
     p.add_argument("--skip-cpu", action="store_true")
-    p.add_argument("--only", choices=["cartpole", "legged", "aba"], default=None,
+    p.add_argument("--only", choices=["cartpole", "legged", "aba", "steps"], default=None,
                    help="run one block: the CartPole headline, the legged rollouts (then the line's value is the "
-                        "legged4 S = 8 rollout), or the ABA Euler step (for counter collection; no line)")
+                        "legged4 S = 8 rollout), the ABA Euler step, or the ABA Euler step and the other step "
+                        "bodies (the last two for counter collection; no line)")
     p.add_argument("--legged-n", type=int, default=262144)
     p.add_argument("--legged-horizon", type=int, default=1000)
     p.add_argument("--sweep", action="store_true", help="also run the CartPole N = 2^0..2^24 sweep")
@@ -970,9 +971,11 @@ def main():
                 log(f"legged{c} numpy baseline: {rate:,.0f} env-steps/s -> GPU/CPU "
                     f"{legged['speedup_vs_cpu_s8']:,.0f}x")
             extra[f"legged{c}_es_rollout"] = legged
-    if args.only == "aba":
+    if args.only in ("aba", "steps"):
         extra["aba_euler"] = bench_aba(dev)
-        print(json.dumps({"aba_euler": extra["aba_euler"]}), flush=True)
+        if args.only == "steps":
+            extra["step_bodies"] = bench_step_bodies(dev)
+        print(json.dumps(extra), flush=True)
         return
     if args.only is None:
         extra["es_config2"] = bench_es_config2(dev, args.repeats)
