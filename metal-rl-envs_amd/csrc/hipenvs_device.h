@@ -305,7 +305,7 @@ int resident_blocks_per_cu(Kernel kernel, int* per_cu) {
   static std::mutex lock;
   int dev = 0;
   const int status = current_device(&dev);
-  if (status != 0) return status;
+  if (status != HIPENVS_OK) return status;
   if (!ready[dev].load(std::memory_order_acquire)) {
     std::lock_guard<std::mutex> guard(lock);
     if (!ready[dev].load(std::memory_order_relaxed)) {
@@ -313,14 +313,14 @@ int resident_blocks_per_cu(Kernel kernel, int* per_cu) {
       const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64, 0);
       if (e != hipSuccess) {
         set_last_hip_error((int)e);
-        return -3;  // HIPENVS_E_HIP
+        return HIPENVS_E_HIP;
       }
       cache[dev] = blocks > 0 ? blocks : 1;
       ready[dev].store(1, std::memory_order_release);
     }
   }
   *per_cu = cache[dev];
-  return 0;
+  return HIPENVS_OK;
 }
 
 inline unsigned grid_for(int64_t items, int block = kBlock) {
