@@ -673,10 +673,13 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
     if (g + G * u < HID) xh[g + G * u] = hs[u];
   __syncthreads();
   // lane g sums heads g, g + G, ... over the hidden values in order; a head's HID weights are
-  // loaded together (one memory round trip per head), from an opaque copy of the address so
-  // that the loads stay here (not hoisted out of the caller's step loop)
-  const float* wh = w;
-  asm volatile("" : "+v"(wh));
+  // loaded together (one memory round trip per head), at an offset the compiler cannot see
+  // (zero) so that the loads stay here, not hoisted out of the caller's step loop; offsetting
+  // w keeps the loads global (an opaque pointer would make them flat loads, which also wait
+  // with the LDS traffic)
+  int opaque_zero = 0;
+  asm volatile("" : "+s"(opaque_zero));
+  const float* wh = w + opaque_zero;
 #pragma unroll
   for (int o = g; o < OUT; o += G) {
     float w2r[HID];
@@ -965,7 +968,8 @@ constexpr int kGroupMembers = 64 / kGroupLanes;
 // VGPRs at C = 2 (H = 64), so two waves share a SIMD and the tail takes over at twice the
 // survivors per CU; at C = 4 it needs 256 + 66 AGPRs, one wave per SIMD. (Reloading the
 // weights every step instead fits two waves at C = 4, 206 VGPRs, but the ES rollout at
-// N = 262,144 and 8 sweeps took 60.8 instead of 50.9 ms.)
+// N = 262,144 and 8 sweeps took 60.6 instead of 50.0 ms: a SIMD holding two long-lived
+// members' waves steps each at half speed to the end of the horizon.)
 template <int C>
 constexpr int kTailWaves = C <= 2 ? 2 : 1;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
