@@ -969,7 +969,7 @@ constexpr int kGroupMembers = 64 / kGroupLanes;
 // survivors per CU; at C = 4 it needs 256 + 66 AGPRs, one wave per SIMD. (Reloading the
 // weights every step instead fits two waves at C = 4, 206 VGPRs, but the ES rollout at
 // N = 262,144 and 8 sweeps took 60.6 instead of 50.0 ms: a SIMD holding two long-lived
-// members' waves steps each at half speed to the end of the horizon.)
+// members' waves steps each at part speed to the end of the horizon.)
 template <int C>
 constexpr int kTailWaves = C <= 2 ? 2 : 1;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
