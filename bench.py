@@ -91,14 +91,18 @@ FP32_UNPACKED_TFLOPS = 78.6        # one FMA per lane per cycle
 CARTPOLE_BYTES = 41
 # HBM bytes per launch: rocprofv3 --pmc FETCH_SIZE and then WRITE_SIZE (one counter per run)
 # over `bench.py --only cartpole --skip-cpu --steps 32 --warmup 2 --repeats 1 --region-seconds
-# 0.0001 --copy-mib 256`, `bench.py --only aba --skip-cpu --copy-mib 256` and `bench.py --only
-# legged --skip-cpu --repeats 1 --copy-mib 256`, in KiB per dispatch. The same counters read
+# 0.0001 --copy-mib 256`, `bench.py --only aba --skip-cpu --copy-mib 256` (`--only steps` for the
+# step bodies) and `bench.py --only legged --skip-cpu --repeats 1 --copy-mib 256`, in KiB per
+# dispatch. The same counters read
 # 131085.3 and 262144.0 KiB for the 256 MiB device copy in the same process, so FETCH_SIZE is
 # scaled by 2.000 and WRITE_SIZE by 1.000. Algorithmic bytes: 41 x N for the CartPole step.
 # Tables and commands: profiles/cartpole_step_n262144.md, profiles/aba_euler_n65536.md,
-# profiles/legged_es_rollout_n262144.md.
+# profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
 ABA_TRAFFIC = {4: 4654910, 16: 17652928, 64: 119529808}
+STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k8": 9770478,
+                     "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
+                     "legged4_s8_reference": 16402572}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
 LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110160000000, (4, 8): 125670000000, (4, 16): 139980000000,
                           (2, 4): 58598000000, (2, 8): 64125000000, (2, 16): 89396000000}
@@ -918,7 +922,7 @@ def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
         out[name] = {"n_envs": n, "steps": steps, "env_steps_per_s": n * steps / wall, "us_per_launch": launch * 1e6,
                      "bytes_per_env_step": bytes_step,
                      "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                  "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
+                                  "frac": achieved / HBM_PEAK_GBS, "traffic": STEP_BODY_TRAFFIC.get(name)}}
         log(f"{name} step N={n}: {n * steps / wall:,.0f} env-steps/s, {launch * 1e6:.2f} us per launch")
         del g, bufs, actions
     return out
