@@ -99,7 +99,7 @@ CARTPOLE_BYTES = 41
 # Tables and commands: profiles/cartpole_step_n262144.md, profiles/aba_euler_n65536.md,
 # profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
-ABA_TRAFFIC = {4: 4654910, 16: 17652928, 64: 119529808}
+ABA_TRAFFIC = {4: 4654925, 16: 17652919, 64: 100206816}
 STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k8": 9770478,
                      "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
                      "legged4_s8_reference": 16402572}

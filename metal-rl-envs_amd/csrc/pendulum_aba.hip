@@ -336,7 +336,15 @@ __global__ __launch_bounds__(kBlock) void step_euler_kernel(const float* __restr
 #ifndef ABA_STAGE_LINKS
 #define ABA_STAGE_LINKS 4
 #endif
-constexpr int kStageLinks = ABA_STAGE_LINKS;  // links whose LDS rows one pass may read ahead
+// The staged K = 64 kernel's passes read their LDS rows (and the last pass its inputs)
+// kStageLinks links ahead of their use, and hold later reads back with a memory barrier
+// every kStageLinks links; its first pass reads its inputs kOutwardAhead links ahead. 2, 8
+// or 16 instead of 4 change the K = 64 step by 1.2 us or less (54.2 us at N = 65,536).
+constexpr int kStageLinks = ABA_STAGE_LINKS;
+#ifndef ABA_OUTWARD_AHEAD
+#define ABA_OUTWARD_AHEAD 4
+#endif
+constexpr int kOutwardAhead = ABA_OUTWARD_AHEAD;
 
 // A (rows, n) float32 array seen by one env through a buffer resource: row r of env e is
 // at byte (r * n + e) * 4, addressed as a per-lane offset e * 4 plus a uniform row offset in
@@ -359,16 +367,19 @@ struct RowBuffer {
   }
 };
 
-// The Euler step for long chains with the per-link state staged by lifetime. The chain's
-// passes keep, per link: cos/sin of the joint angle (all three passes), the link velocity
-// (outward to inward), the velocity-product terms c1, c2 (outward to last), and U, u (inward
-// to last). At K = 64 the step of the generic form holds the input angles and velocities
-// and every per-link array for the whole step, about 790 floats per lane, and spills past
-// the 512 registers. Here the inputs are read as the outward pass consumes them and again
-// for the final update, cos/sin sit in LDS (one 4-byte slot per link and thread, 2 * K * 4 *
-// kBlock bytes per workgroup), and c1, c2 are formed once in the outward pass, so at most
-// about 384 floats per lane are live. Every value is the generic form's, from the same
-// operations in the same order (accelerations, euler, terminal, store_with_reset).
+// The Euler step for long chains with the per-link state staged by lifetime. At K = 64 the
+// step of the generic form holds the input angles and velocities and every per-link array
+// for the whole step, about 790 floats per lane, and spills past the 512 registers. Here:
+// - cos/sin of the joint angles sit in LDS (one 4-byte slot per link and thread,
+//   2 * K * 4 * kBlock bytes per workgroup), read by all three passes;
+// - the outward pass keeps, per link, the link velocity and the joint rate qd (4 floats);
+// - the inward pass forms c1, c2 from them as it needs them, and each link it passes
+//   trades those 4 floats for U and u (4 floats), so about 256 floats per lane are live;
+// - the last pass runs the outward velocity recursion again next to the accelerations
+//   (the same operations on the same values, so c1, c2 come out the same bits), rereads
+//   each link's inputs, and finishes the link's Euler update, wrap, clip and cosine there.
+// Every value is the generic form's, from the same operations in the same order
+// (accelerations, euler, terminal, store_with_reset).
 template <int K, bool kArrayTorque>
 __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* __restrict__ state,
                                                                    const float* __restrict__ torque, uint32_t seed,
@@ -382,14 +393,24 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
   float* cs_l = trig_lds + K * kBlock + threadIdx.x;
   const float tq = kArrayTorque ? stream_load(torque + e)
                                 : uniform_pm(pcg_hash(env_hash(seed, (uint32_t)e) + kTorqueOffset), 1.0f);
-  float vw[K], vx[K], vy[K], c1[K], c2[K], U0[K], U1[K], U2[K], uu[K], acc[K];
+  float vw[K], vx[K], vy[K], qdv[K], U0[K], U1[K], U2[K], uu[K];
   const RowBuffer in(state, 2 * K, n, e);
   // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
   {
     float w = 0.0f, x = 0.0f, y = 0.0f, th_prev = 0.0f, om_prev = 0.0f;
+    float th0[K], om0[K];  // the inputs, read kOutwardAhead links ahead of their use
+#pragma unroll
+    for (int j = 0; j < K && j < kOutwardAhead; ++j) {
+      th0[j] = in.load(j);
+      om0[j] = in.load(K + j);
+    }
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      const float th_i = in.load(i), om_i = in.load(K + i);
+      if (i + kOutwardAhead < K) {
+        th0[i + kOutwardAhead] = in.load(i + kOutwardAhead);
+        om0[i + kOutwardAhead] = in.load(K + i + kOutwardAhead);
+      }
+      const float th_i = th0[i], om_i = om0[i];
       const float q = (i == 0) ? th_i : th_i - th_prev;
       const float qd = (i == 0) ? om_i : om_i - om_prev;
       float sn, cs;
@@ -403,8 +424,7 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
       vw[i] = nw;
       vx[i] = nx;
       vy[i] = ny;
-      c1[i] = qd * ny;
-      c2[i] = (-qd) * nx;
+      qdv[i] = qd;
       w = nw;
       x = nx;
       y = ny;
@@ -414,10 +434,18 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
   }
   asm volatile("" ::: "memory");  // each pass reads its LDS rows in its own order, not hoisted into the last
   // inward: articulated inertia and bias folded into the parent (pendulum_aba_np.py:51-82)
+  // Each pass below issues its reads kStageLinks links ahead of their use (rotating
+  // registers), so their latency overlaps the links in between.
+  float cv[K], sv[K];
   {
     float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
     float P0, P1, P2;
     own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
+#pragma unroll
+    for (int j = K - 1; j >= 1 && j > K - 1 - kStageLinks; --j) {
+      cv[j] = cs_l[j * kBlock];
+      sv[j] = sn_l[j * kBlock];
+    }
 #pragma unroll
     for (int i = K - 1; i >= 0; --i) {
       U0[i] = A0;
@@ -425,17 +453,22 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
       U2[i] = A2;
       uu[i] = (i == 0 ? tq : 0.0f) - P0;
       if (i == 0) break;
+      if (i - kStageLinks >= 1) {
+        cv[i - kStageLinks] = cs_l[(i - kStageLinks) * kBlock];
+        sv[i - kStageLinks] = sn_l[(i - kStageLinks) * kBlock];
+      }
       const float D = A0;
       const float I0 = A0 - (A0 * A0) / D, I1 = A1 - (A0 * A1) / D, I2 = A2 - (A0 * A2) / D;
       const float I3 = A3 - (A1 * A1) / D, I4 = A4 - (A1 * A2) / D, I5 = A5 - (A2 * A2) / D;
-      const float Iac0 = I1 * c1[i] + I2 * c2[i];
-      const float Iac1 = I3 * c1[i] + I4 * c2[i];
-      const float Iac2 = I4 * c1[i] + I5 * c2[i];
+      const float c1 = qdv[i] * vy[i], c2 = (-qdv[i]) * vx[i];
+      const float Iac0 = I1 * c1 + I2 * c2;
+      const float Iac1 = I3 * c1 + I4 * c2;
+      const float Iac2 = I4 * c1 + I5 * c2;
       const float g = uu[i] / D;
       const float pa0 = (P0 + Iac0) + A0 * g;
       const float pa1 = (P1 + Iac1) + A1 * g;
       const float pa2 = (P2 + Iac2) + A2 * g;
-      const float c = cs_l[i * kBlock], s = sn_l[i * kBlock];
+      const float c = cv[i], s = sv[i];
       const float B00 = (I0 + I1 * s) + I2 * c, B01 = I1 * c - I2 * s, B02 = I1 * s + I2 * c;
       const float B10 = (I1 + I3 * s) + I4 * c, B11 = I3 * c - I4 * s, B12 = I3 * s + I4 * c;
       const float B20 = (I2 + I4 * s) + I5 * c, B21 = I4 * c - I5 * s, B22 = I4 * s + I5 * c;
@@ -454,40 +487,63 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
     }
   }
   asm volatile("" ::: "memory");
-  // outward: accelerations from a base accelerating at -g (pendulum_aba_np.py:83-99)
+  // The last pass reads the inputs again, through a copy of the pointer that the compiler
+  // cannot see through, so the reads are not hoisted above the passes (the input is
+  // read-only, and a plain memory barrier does not hold its loads back).
+  const float* again = state;
+  asm volatile("" : "+s"(again)::"memory");
+  const RowBuffer in2(again, 2 * K, n, e), out(next, 2 * K, n, e);
+  // outward: accelerations from a base accelerating at -g (pendulum_aba_np.py:83-99), with
+  // the velocity recursion of the first pass repeated for c1, c2, and each link's
+  // semi-implicit Euler update, wrap, clip and cosine for the termination test
+  float cos_sum = 0.0f;
   {
     float aw = 0.0f, ax = -GRAVITY, ay = 0.0f, run = 0.0f;
+    float w = 0.0f, x = 0.0f, y = 0.0f, om_prev = 0.0f;
+    float thv[K], omv[K];
+#pragma unroll
+    for (int j = 0; j < K && j < kStageLinks; ++j) {
+      thv[j] = in2.load(j);
+      omv[j] = in2.load(K + j);
+      cv[j] = cs_l[j * kBlock];
+      sv[j] = sn_l[j * kBlock];
+    }
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      const float c = cs_l[i * kBlock], s = sn_l[i * kBlock];
+      if (i + kStageLinks < K) {
+        thv[i + kStageLinks] = in2.load(i + kStageLinks);
+        omv[i + kStageLinks] = in2.load(K + i + kStageLinks);
+        cv[i + kStageLinks] = cs_l[(i + kStageLinks) * kBlock];
+        sv[i + kStageLinks] = sn_l[(i + kStageLinks) * kBlock];
+      }
+      const float th_i = thv[i], om_i = omv[i];
+      const float qd = (i == 0) ? om_i : om_i - om_prev;
+      const float c = cv[i], s = sv[i];
+      const float vxy = (i == 0) ? (y + w * 0.0f) : (y + w);
+      const float nw = w + qd;
+      const float nx = c * x + s * vxy;
+      const float ny = (-s) * x + c * vxy;
+      w = nw;
+      x = nx;
+      y = ny;
+      const float c1 = qd * ny, c2 = (-qd) * nx;
       const float xy = (i == 0) ? (ay + aw * 0.0f) : (ay + aw);
       const float ap0 = aw;
-      const float ap1 = (c * ax + s * xy) + c1[i];
-      const float ap2 = ((-s) * ax + c * xy) + c2[i];
+      const float ap1 = (c * ax + s * xy) + c1;
+      const float ap2 = ((-s) * ax + c * xy) + c2;
       const float qdd = (uu[i] - ((U0[i] * ap0 + U1[i] * ap1) + U2[i] * ap2)) / U0[i];
       aw = ap0 + qdd;
       ax = ap1;
       ay = ap2;
       run = run + qdd;
-      acc[i] = run;
+      const float om_new = om_i + DT_EULER * run;
+      const float th_new = wrap(th_i + DT_EULER * om_new);
+      out.store(i, th_new);
+      out.store(K + i, clip(om_new, -MAX_VEL, MAX_VEL));
+      cos_sum = (i == 0) ? det_cos(th_new) : cos_sum + det_cos(th_new);
+      om_prev = om_i;
       if ((i & (kStageLinks - 1)) == kStageLinks - 1) asm volatile("" ::: "memory");
     }
-  }
-  // The final update reads the inputs again. The reads go through a copy of the pointer
-  // that the compiler cannot see through, so they are not hoisted above the passes (the
-  // input is read-only, and a plain memory barrier does not hold its loads back).
-  const float* again = state;
-  asm volatile("" : "+s"(again)::"memory");
-  const RowBuffer in2(again, 2 * K, n, e), out(next, 2 * K, n, e);
-  // semi-implicit Euler, wrap, clip, termination, masked reset
-  float cos_sum = 0.0f;
-#pragma unroll
-  for (int p = 0; p < K; ++p) {
-    const float om_new = in2.load(K + p) + DT_EULER * acc[p];
-    const float th_new = wrap(in2.load(p) + DT_EULER * om_new);
-    out.store(p, th_new);
-    out.store(K + p, clip(om_new, -MAX_VEL, MAX_VEL));
-    cos_sum = (p == 0) ? det_cos(th_new) : cos_sum + det_cos(th_new);
   }
   const bool d = -cos_sum > (float)K * 0.5f;
   if (d) {  // angles U[+-0.1], zero velocities, overwriting the stepped state
