@@ -911,6 +911,52 @@ __global__ __launch_bounds__(64, LEGGED_ROLLOUT_MIN_WAVES) void evaluate_kernel(
   fitness[e] = total;
 }
 
+// Survivor weight copies. A one-row-at-a-time copy waits out a memory round trip per row
+// (the compiler may not move a row's load above the previous row's store, which it cannot
+// prove disjoint). These load kCopyBatch rows into registers before storing them, through
+// pointers declared disjoint, so a member's D rows take D / kCopyBatch round trips.
+constexpr int kCopyBatch = 32;
+
+// n rows, row r at src[r * src_stride] -> dst[r * dst_stride]
+__device__ __forceinline__ void copy_rows(float* __restrict__ dst, int64_t dst_stride,
+                                          const float* __restrict__ src, int64_t src_stride, int n) {
+  int r = 0;
+  for (; r + kCopyBatch <= n; r += kCopyBatch) {
+    float b[kCopyBatch];
+#pragma unroll
+    for (int i = 0; i < kCopyBatch; ++i) b[i] = src[(r + i) * src_stride];
+#pragma unroll
+    for (int i = 0; i < kCopyBatch; ++i) dst[(r + i) * dst_stride] = b[i];
+  }
+  for (; r < n; ++r) dst[r * dst_stride] = src[r * src_stride];
+}
+
+// A member's weights from the caller's FlatRows columns (row stride src_stride) to a
+// UnitRows tile (row stride dst_stride): hidden unit j's 1 + OBS + OUT rows at a time.
+template <int OBS, int HID, int OUT>
+__device__ __forceinline__ void copy_flat_to_units(float* __restrict__ dst, int64_t dst_stride,
+                                                   const float* __restrict__ src, int64_t src_stride) {
+  using F = FlatRows<OBS, HID, OUT>;
+  using T = UnitRows<OBS, HID, OUT>;
+  constexpr int kUnit = T::kUnit;
+#pragma unroll 2
+  for (int j = 0; j < HID; ++j) {
+    float b[kUnit];
+    b[0] = src[F::b1(j) * src_stride];
+#pragma unroll
+    for (int k = 0; k < OBS; ++k) b[1 + k] = src[F::w1(k, j) * src_stride];
+#pragma unroll
+    for (int o = 0; o < OUT; ++o) b[1 + OBS + o] = src[F::w2(j, o) * src_stride];
+#pragma unroll
+    for (int r = 0; r < kUnit; ++r) dst[(T::b1(j) + r) * dst_stride] = b[r];
+  }
+  float b2[OUT];
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) b2[o] = src[F::b2(o) * src_stride];
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) dst[T::b2(o) * dst_stride] = b2[o];
+}
+
 // Compacting schedule for the fused rollout. Episode lengths are heavy-tailed
 // (at the ES benchmark's shape the mean is ~43 steps while a few members last
 // the whole horizon), and a one-member-per-lane launch keeps each wave busy
@@ -1065,7 +1111,7 @@ __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& d
             dst.meta[cap + to] = t;
           }
           float* wd = dst.theta + (to / kTile) * (int64_t)D * kTile + (to % kTile);
-          for (int d = g; d < D; d += G) wd[d * kTile] = w[d * kTile];
+          copy_rows(wd + g * kTile, (int64_t)G * kTile, w + g * kTile, (int64_t)G * kTile, (D - g + G - 1) / G);
         }
       }
     }
@@ -1201,18 +1247,10 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
         dst.meta[slot] = id;
         dst.meta[cap + slot] = t;
         float* wd = dst.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
-        if constexpr (kFirst) {  // caller's FlatRows columns -> UnitRows tile
-          using F = FlatRows<OBS, HID, OUT>;
-          using T = UnitRows<OBS, HID, OUT>;
-          for (int j = 0; j < HID; ++j) {
-            wd[T::b1(j) * kTile] = w[F::b1(j) * src_stride];
-            for (int k = 0; k < OBS; ++k) wd[T::w1(k, j) * kTile] = w[F::w1(k, j) * src_stride];
-            for (int o = 0; o < OUT; ++o) wd[T::w2(j, o) * kTile] = w[F::w2(j, o) * src_stride];
-          }
-          for (int o = 0; o < OUT; ++o) wd[T::b2(o) * kTile] = w[F::b2(o) * src_stride];
-        } else {  // tile -> tile, same rows
-          for (int d = 0; d < D; ++d) wd[d * kTile] = w[d * kTile];
-        }
+        if constexpr (kFirst)  // caller's FlatRows columns -> UnitRows tile
+          copy_flat_to_units<OBS, HID, OUT>(wd, kTile, w, src_stride);
+        else  // tile -> tile, same rows
+          copy_rows(wd, kTile, w, kTile, D);
       }
     }
   }
