@@ -385,10 +385,11 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         cB[k][l] = nrow ? Ann[k][l] : Atn[k][l];
       }
       w0x[k] = nrow ? w0n[k] : w0t[k];
-      // numerators P * X + Q * Y: lane 0 Att tw + Atn wt; lane 1 (-Ann) wt + (-Atn) tw, which is
-      // the reference's (-Ann) wt - Atn tw exactly (a - b = a + (-b), and the sum commutes)
-      qP[k] = nrow ? -blk[k].Ann : blk[k].Att;
-      qQ[k] = nrow ? -blk[k].Atn : blk[k].Atn;
+      // numerators qP * wt + qQ * tw: lane 0 Atn wt + Att tw, which is the reference's
+      // Att tw + Atn wt (a rounded sum commutes); lane 1 (-Ann) wt + (-Atn) tw, which is
+      // the reference's (-Ann) wt - Atn tw exactly (a - b = a + (-b))
+      qP[k] = nrow ? -blk[k].Ann : blk[k].Atn;
+      qQ[k] = nrow ? -blk[k].Atn : blk[k].Att;
       qd[k] = (g == 2) ? blk[k].den_p : (g == 3) ? blk[k].den_m : blk[k].det;
       qr[k] = (g == 2) ? blk[k].rden_p : (g == 3) ? blk[k].rden_m : blk[k].rdet;
       slipc[k] = blk[k].Att * MU + blk[k].Atn;
@@ -418,8 +419,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         const bool touching = depth[k] >= 0.0f;
         const float target = BAUMGARTE_OVER_H * max0(depth[k]);
         const float tw = target - wn;
-        const float X = nrow ? wt : tw, Y = nrow ? tw : wt;
-        const float num = (g == 2 || g == 3) ? tw : qP[k] * X + qQ[k] * Y;
+        const float num = (g == 2 || g == 3) ? tw : qP[k] * wt + qQ[k] * tw;
         const float quo = div(num, qd[k], qr[k]);
         const float ln_stick = group_bcast<0>(quo);
         const float lt_stick = group_bcast<1>(quo);
