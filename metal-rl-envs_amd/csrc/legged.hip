@@ -121,6 +121,15 @@ __device__ __forceinline__ void row_trig(float sn, float cs, float* sa, float* c
   }
 }
 
+// out[i] = lane i's x, for i < K, on every lane of the 16-lane row.
+template <int K>
+__device__ __forceinline__ void row_gather(float x, float* out) {
+  if constexpr (K > 0) {
+    row_gather<K - 1>(x, out);
+    out[K - 1] = group_bcast<K - 1>(x);
+  }
+}
+
 // One semi-implicit Euler substep with block PGS contacts, in place (legged_np.py:57-97).
 // kGroup = 0: one lane computes the whole substep. kGroup = G > 0: the G lanes g = 0..G-1 of
 // a member's group (one 16-lane DPP row) all hold the member's state and compute everything
@@ -471,6 +480,26 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         MiJn[k][i] = xs[((C + k) * N + i) * 64];
       }
     }
+  } else if constexpr (kGroup == 16 && !kHopperSum) {
+    // lane i < N forms velocity i (its sum over the contacts in the same order as below,
+    // from its own column of the solved rows) and the row broadcast gives it to the group
+    constexpr int kRow = 8;
+    asm volatile("" ::: "memory");  // read here, not held in registers through the sweeps
+    const int i = g < N ? g : 0;  // lanes past N form velocity 0 again, unused
+    float vfi = vf[0];
+#pragma unroll
+    for (int r = 1; r < N; ++r) vfi = (i == r) ? vf[r] : vfi;
+    float si = xs[(1 + 0) * kRow + i] * lt[0] + xs[(1 + C + 0) * kRow + i] * ln[0];
+#pragma unroll
+    for (int k = 1; k < C; ++k) si = si + (xs[(1 + k) * kRow + i] * lt[k] + xs[(1 + C + k) * kRow + i] * ln[k]);
+    float vn[N];
+    row_gather<N>(vfi + si, vn);
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      v[r] = vn[r];
+      q[r] = q[r] + H * vn[r];
+    }
+    return;
   } else if constexpr (kGroup > 0) {
     constexpr int kRow = 8;
     asm volatile("" ::: "memory");  // read here, not held in registers through the sweeps
