@@ -1047,6 +1047,12 @@ constexpr int kGroupMembers = 64 / kGroupLanes;
 // members' waves steps each at part speed to the end of the horizon.)
 template <int C>
 constexpr int kTailWaves = C <= 2 ? 2 : 1;
+// Whether chunks between the tail's bound and LEGGED_GROUP_CHUNK_MEMBERS_PER_CU run in the
+// group form. At C <= 2 the tail already takes over at 32 per CU, and one member per lane
+// down to there was faster (biped ES rollout at N = 262,144: 28.0 -> 27.5 ms at 8 sweeps,
+// 40.2 -> 38.2 ms at 16; the 8-lane group kernel needs 256 registers and spills at C = 2).
+template <int C>
+constexpr bool kGroupChunks = C > 2;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
 template <int C>
 constexpr int kBlockFloats = 4 * C * C + 12 * C;
@@ -1364,7 +1370,7 @@ template <int C>
 inline GroupBounds group_bounds(int64_t p, int cus) {
   GroupBounds b;
   b.wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * kTailWaves<C> * cus;
-  const int64_t gm = (int64_t)LEGGED_GROUP_CHUNK_MEMBERS_PER_CU * cus;
+  const int64_t gm = kGroupChunks<C> ? (int64_t)LEGGED_GROUP_CHUNK_MEMBERS_PER_CU * cus : 0;
   b.group_max = gm > b.wide_max ? gm : b.wide_max;
   // one member group per workgroup: a kernel never holds more than min(p, its bound) members
   const int64_t group_members = p < b.group_max ? p : b.group_max;
@@ -1386,10 +1392,12 @@ int launch_later_chunk(const float* state0, const float* theta0, int64_t p, cons
   hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, false>), dim3((unsigned)grid), dim3(64), 0, s, state0, theta0, p,
                      src, dst, cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
                      gb.group_max);
-  if (gb.group_max > gb.wide_max)
-    hipLaunchKernelGGL((rollout_group_chunk_kernel<C, HID, kChunkGroupLanes>), dim3((unsigned)gb.group_grid), dim3(64), 0, s, src, dst,
-                       cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps, gb.wide_max,
-                       gb.group_max);
+  if constexpr (kGroupChunks<C>) {
+    if (gb.group_max > gb.wide_max)
+      hipLaunchKernelGGL((rollout_group_chunk_kernel<C, HID, kChunkGroupLanes>), dim3((unsigned)gb.group_grid), dim3(64), 0,
+                         s, src, dst, cap, chunk_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
+                         gb.wide_max, gb.group_max);
+  }
   hipLaunchKernelGGL((rollout_tail_kernel<C, HID>), dim3((unsigned)gb.tail_grid), dim3(64), 0, s, src, cap, horizon,
                      iters, alive, fall, gate, af, ad, fitness, steps, gb.wide_max);
   return launch_status();

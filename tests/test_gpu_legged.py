@@ -160,13 +160,14 @@ def test_group_tail_equals_static(dev, c, hidden, iters):
         assert ss.max().item() > 8  # members outlived the first chunk
 
 
-@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (2, 32, 8), (4, 64, 8), (2, 64, 4), (4, 64, 16)])
+@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (2, 32, 8), (4, 64, 8), (2, 64, 4), (4, 64, 16),
+                                            (4, 4, 8), (4, 32, 8)])
 def test_group_chunk_equals_static(dev, c, hidden, iters):
     """Populations above the group tail's bound (16 members per CU at C = 4, 32 at C <= 2,
-    where the tail runs two waves per SIMD) and within the group chunk's (48 per CU), so
-    later chunks run in the group form (8 lanes per member: two solves, two Delassus blocks
-    and up to two heads per lane) and append their survivors until the count falls to the
-    tail's bound: member for member equal to the one-lane kernel."""
+    where the tail runs two waves per SIMD) and within 48 per CU. At C = 4 later chunks run
+    in the group form (8 lanes per member: two solves, two Delassus blocks and up to two
+    heads per lane), at C <= 2 one member per lane; either appends its survivors until the
+    count falls to the tail's bound: member for member equal to the one-lane kernel."""
     from hipenvs import legged, legged_rollout
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -182,7 +183,7 @@ def test_group_chunk_equals_static(dev, c, hidden, iters):
                                         iters=iters)
         assert torch.equal(fq, fs) and torch.equal(sq, ss), (c, hidden, assist)
         past_first = max(past_first, int((ss > 8).sum().item()))
-    assert past_first > tail_per_cu * cus  # the second chunk ran in the group form
+    assert past_first > tail_per_cu * cus  # the second chunk ran above the tail's bound
 
 
 def test_shaped_reward_and_assist_match_oracle(dev):
