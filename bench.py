@@ -104,8 +104,8 @@ STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k
                      "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
                      "legged4_s8_reference": 16402572}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110180000000, (4, 8): 125690000000, (4, 16): 139980000000,
-                          (2, 4): 49790000000, (2, 8): 50912000000, (2, 16): 58846000000}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110180000000, (4, 8): 125700000000, (4, 16): 139990000000,
+                          (2, 4): 40943000000, (2, 8): 42357000000, (2, 16): 49671000000}
 
 
 def log(msg):
@@ -548,8 +548,9 @@ def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
     theta_cols = theta.T.contiguous()
     state = legged.Legged(c).reset(p, seed=0, device=dev)
     d = legged_rollout.n_params(hidden, c)
+    first = ", the first 16" if c <= 2 else ""
     out = {"n_envs": p, "c": c, "hidden": hidden, "horizon": horizon, "sigma": 0.03, "alive_bonus": 1.0,
-           "schedule": f"chunked ({legged_rollout.CHUNK_STEPS} steps), columns layout", "by_sweeps": {}}
+           "schedule": f"chunked ({legged_rollout.CHUNK_STEPS} steps{first}), columns layout", "by_sweeps": {}}
     for s in sweeps_list:
         wall, ev, taken, fit_mean, alive = time_rollout(state, theta_cols, hidden, horizon, c, s, "chunked",
                                                         args.repeats, alive_at=ALIVE_AT)

@@ -240,7 +240,8 @@ int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iters, int32_t 
  * or hidden. */
 int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t hidden, int64_t p);
 
-/* The same rollout, scheduled in chunks of `chunk_steps` steps: after each
+/* The same rollout, scheduled in chunks of `chunk_steps` steps (for c <= 2 the
+ * first chunk is 16 steps when chunk_steps is longer): after each
  * chunk the surviving members (state, accumulators and weights) are packed
  * into a dense column buffer in `workspace`, so later chunks run full waves
  * despite heavy-tailed episode lengths; the counts stay on the device and the

@@ -10,7 +10,8 @@ pays ``fall_penalty`` once. Returns (fitness, steps taken).
 Additions: ``iters`` (the reference fixes ITERS = 8 at build time) and
 ``schedule``:
 
-* "chunked" (default): the rollout runs in chunks of ``chunk_steps`` steps and
+* "chunked" (default): the rollout runs in chunks of ``chunk_steps`` steps (for
+  ``c <= 2`` a first chunk of 16 when ``chunk_steps`` is longer) and
   the survivors of each chunk (state, accumulators, weights) are packed into a
   dense column buffer before the next. Episode lengths are heavy-tailed (mean
   ~43 steps at the benchmark's shape while a few members last the whole
