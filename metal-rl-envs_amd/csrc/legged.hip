@@ -615,6 +615,10 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
 #endif
 template <int C>
 constexpr int32_t kFirstChunkSteps = C <= 2 ? LEGGED_BIPED_FIRST_CHUNK_STEPS : 0;
+template <int C>
+inline int32_t first_chunk_steps(int32_t chunk_steps) {
+  return kFirstChunkSteps<C> > 0 && kFirstChunkSteps<C> < chunk_steps ? kFirstChunkSteps<C> : chunk_steps;
+}
 
 // POLICY_UNROLL hidden units per policy loop iteration bounds how many of the member's
 // weight loads are in flight at once.
@@ -1447,8 +1451,7 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   const int64_t needed = (p + 63) / 64;
   int64_t resident = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
   const float af = (float)assist, ad = (float)(0.1 * assist);
-  const int32_t first_steps =
-      kFirstChunkSteps<C> > 0 && kFirstChunkSteps<C> < chunk_steps ? kFirstChunkSteps<C> : chunk_steps;
+  const int32_t first_steps = first_chunk_steps<C>(chunk_steps);
   // first chunk: the caller's arrays -> set 0
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
   const GroupBounds gb = group_bounds<C>(p, cus);
@@ -1505,7 +1508,7 @@ int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uin
                      seed, sigma, set[0], cap);
   int status = launch_status();
   int cur = 0;
-  int32_t len = kFirstChunkSteps<C> > 0 && kFirstChunkSteps<C> < chunk_steps ? kFirstChunkSteps<C> : chunk_steps;
+  int32_t len = first_chunk_steps<C>(chunk_steps);
   for (int64_t done = 0; status == HIPENVS_OK && done < horizon; done += len, len = chunk_steps) {
     status = launch_later_chunk<C, HID>(state, theta, p, set[cur], set[1 - cur], cap, grid, gb, len, horizon, iters,
                                         alive, fall, gate, af, ad, fitness, steps, s);
