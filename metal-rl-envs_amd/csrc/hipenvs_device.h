@@ -178,6 +178,30 @@ __device__ __forceinline__ float group_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xF, 0xF, false));
 }
 
+// Lane L (< 8) of each 8-lane half of every 16-lane row, on every lane of that half: how an
+// 8-lane group shares a value. Two DPP row broadcasts of v: lane L into the first half
+// (banks 0 and 1), then lane 8 + L into the second (banks 2 and 3; the first half keeps
+// what the first move wrote). Neither reads the other's result, so no wait states sit
+// between them.
+template <int L>
+__device__ __forceinline__ float half_bcast(float v) {
+  static_assert(L >= 0 && L < 8, "a lane of the 8-lane half");
+  const int x = __float_as_int(v);
+  const int lo = __builtin_amdgcn_mov_dpp(x, 0x150 + L, 0xF, 0x3, false);
+  return __int_as_float(__builtin_amdgcn_update_dpp(lo, x, 0x150 + 8 + L, 0xF, 0xC, false));
+}
+
+// Lane L of each G-lane group (G = 8 or 16) on every lane of that group.
+template <int G, int L>
+__device__ __forceinline__ float lane_bcast(float v) {
+  static_assert(G == 8 || G == 16, "groups of 8 or 16 lanes");
+  if constexpr (G == 16) {
+    return group_bcast<L>(v);
+  } else {
+    return half_bcast<L>(v);
+  }
+}
+
 __device__ __forceinline__ float det_sin(float x) {
   float s, c;
   det_sincos(x, &s, &c);

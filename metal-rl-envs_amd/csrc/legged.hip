@@ -111,30 +111,32 @@ __device__ __forceinline__ void chol_solve(const float (&L)[N][N], const double 
   }
 }
 
-// sa[k], ca[k] = lane k's sn, cs, for k < K, on every lane of the 16-lane row.
-template <int K>
+// sa[k], ca[k] = lane k's sn, cs, for k < K, on every lane of the G-lane group.
+template <int G, int K>
 __device__ __forceinline__ void row_trig(float sn, float cs, float* sa, float* ca) {
   if constexpr (K > 0) {
-    row_trig<K - 1>(sn, cs, sa, ca);
-    sa[K - 1] = group_bcast<K - 1>(sn);
-    ca[K - 1] = group_bcast<K - 1>(cs);
+    row_trig<G, K - 1>(sn, cs, sa, ca);
+    sa[K - 1] = lane_bcast<G, K - 1>(sn);
+    ca[K - 1] = lane_bcast<G, K - 1>(cs);
   }
 }
 
-// out[i] = lane i's x, for i < K, on every lane of the 16-lane row.
-template <int K>
+// out[i] = lane i's x, for i < K, on every lane of the G-lane group.
+template <int G, int K>
 __device__ __forceinline__ void row_gather(float x, float* out) {
   if constexpr (K > 0) {
-    row_gather<K - 1>(x, out);
-    out[K - 1] = group_bcast<K - 1>(x);
+    row_gather<G, K - 1>(x, out);
+    out[K - 1] = lane_bcast<G, K - 1>(x);
   }
 }
 
 // One semi-implicit Euler substep with block PGS contacts, in place (legged_np.py:57-97).
-// kGroup = 0: one lane computes the whole substep. kGroup = G > 0: the G lanes g = 0..G-1 of
-// a member's group (one 16-lane DPP row) all hold the member's state and compute everything
-// identically, except that lane g < C evaluates foot g's sin and cos, shared by row
-// broadcast, and lane g < 2C + 1 solves right-hand side g of the 2C + 1 triangular solves
+// kGroup = 0: one lane computes the whole substep. kGroup = G (8 or 16): the G lanes
+// g = 0..G-1 of a member's group (a 16-lane DPP row or half of one) all hold the member's
+// state and compute everything identically, except that lane g < C evaluates foot g's sin
+// and cos, shared by DPP broadcast, the Gauss-Seidel sweeps and the velocity update split
+// their independent work over the lanes (below), and lane g solves right-hand sides g,
+// g + G, ... of the 2C + 1 triangular solves
 // (the forces, then the tangent, then the normal Jacobian rows), exchanged through the
 // group's LDS rows xs ((2C + 1) x 8 floats). Every value is computed by the same expression
 // as in the one-lane form, so the results are the same bits. Callers keep the group's
@@ -152,15 +154,15 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
                                         int g = 0, float* xd = nullptr) {
   constexpr int N = 3 + C;
   float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
-  if constexpr (kGroup == 16) {
-    // lane g < C evaluates foot g's sin and cos; the group's 16 lanes are one DPP row
-    static_assert(C <= 16, "one lane per foot");
+  if constexpr (kGroup == 8 || kGroup == 16) {
+    // lane g < C evaluates foot g's sin and cos, shared by DPP broadcast within the group
+    static_assert(C <= kGroup, "one lane per foot");
     float a = q[2] + q[3];
 #pragma unroll
     for (int k = 1; k < C; ++k) a = (g == k) ? q[2] + q[3 + k] : a;
     float sn, cs;
     det_sincos(a, &sn, &cs);
-    row_trig<C>(sn, cs, sa, ca);
+    row_trig<kGroup, C>(sn, cs, sa, ca);
   } else {
 #pragma unroll
     for (int k = 0; k < C; ++k) det_sincos(q[2] + q[3 + k], &sa[k], &ca[k]);
@@ -376,12 +378,12 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       blk[k] = contact_block(Att[k][k], Atn[k][k], Ann[k][k]);
     }
   }
-  if constexpr (kGroup == 16) {
-    // The member's 16 lanes split each contact's independent work and share the results by
-    // row broadcast: lane 1 forms the normal coupling sum and every other lane the tangential
+  if constexpr (kGroup == 8 || kGroup == 16) {
+    // The member's lanes split each contact's independent work and share the results by
+    // DPP broadcast: lane 1 forms the normal coupling sum and every other lane the tangential
     // one (each with its own coefficient rows), and lanes 0-3 form the four quotients of the
     // contact solve, ln_stick, lt_stick, (target - wn) / den_p and (target - wn) / den_m
-    // (lanes 4-15 repeat lane 0's). Every broadcast value is the expression the one-lane
+    // (lanes 4 and up repeat lane 0's). Every broadcast value is the expression the one-lane
     // sweep evaluates, so the impulses are the same bits.
     const bool nrow = (g == 1);
     float cA[C][C], cB[C][C], w0x[C], qP[C], qQ[C], qd[C], slipc[C];
@@ -421,8 +423,8 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
             first = false;
           }
           const float wx = w0x[k] + sx;
-          wt = group_bcast<0>(wx);
-          wn = group_bcast<1>(wx);
+          wt = lane_bcast<kGroup, 0>(wx);
+          wn = lane_bcast<kGroup, 1>(wx);
         }
         const ContactBlock& b = blk[k];
         const bool touching = depth[k] >= 0.0f;
@@ -430,10 +432,10 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         const float tw = target - wn;
         const float num = (g == 2 || g == 3) ? tw : qP[k] * wt + qQ[k] * tw;
         const float quo = div(num, qd[k], qr[k]);
-        const float ln_stick = group_bcast<0>(quo);
-        const float lt_stick = group_bcast<1>(quo);
-        const float q_p = group_bcast<2>(quo);
-        const float q_m = group_bcast<3>(quo);
+        const float ln_stick = lane_bcast<kGroup, 0>(quo);
+        const float lt_stick = lane_bcast<kGroup, 1>(quo);
+        const float q_p = lane_bcast<kGroup, 2>(quo);
+        const float q_m = lane_bcast<kGroup, 3>(quo);
         const bool sticks = fabsf(lt_stick) <= MU * ln_stick;
         const float ln_p = (b.den_p > 0.0f) ? max0(q_p) : 0.0f;
         const float ln_m = (b.den_m > 0.0f) ? max0(q_m) : 0.0f;
@@ -480,9 +482,10 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         MiJn[k][i] = xs[((C + k) * N + i) * 64];
       }
     }
-  } else if constexpr (kGroup == 16 && !kHopperSum) {
+  } else if constexpr ((kGroup == 8 || kGroup == 16) && !kHopperSum) {
     // lane i < N forms velocity i (its sum over the contacts in the same order as below,
-    // from its own column of the solved rows) and the row broadcast gives it to the group
+    // from its own column of the solved rows) and the DPP broadcast gives it to the group
+    static_assert(3 + C <= kGroup, "one lane per velocity");
     constexpr int kRow = 8;
     asm volatile("" ::: "memory");  // read here, not held in registers through the sweeps
     const int i = g < N ? g : 0;  // lanes past N form velocity 0 again, unused
@@ -493,7 +496,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
 #pragma unroll
     for (int k = 1; k < C; ++k) si = si + (xs[(1 + k) * kRow + i] * lt[k] + xs[(1 + C + k) * kRow + i] * ln[k]);
     float vn[N];
-    row_gather<N>(vfi + si, vn);
+    row_gather<kGroup, N>(vfi + si, vn);
 #pragma unroll
     for (int r = 0; r < N; ++r) {
       v[r] = vn[r];
