@@ -1067,7 +1067,8 @@ constexpr int kTailWaves = C <= 2 ? 2 : 1;
 // Whether chunks between the tail's bound and LEGGED_GROUP_CHUNK_MEMBERS_PER_CU run in the
 // group form. At C <= 2 the tail already takes over at 32 per CU, and one member per lane
 // down to there was faster (biped ES rollout at N = 262,144: 28.0 -> 27.5 ms at 8 sweeps,
-// 40.2 -> 38.2 ms at 16; the 8-lane group kernel needs 256 registers and spills at C = 2).
+// 40.2 -> 38.2 ms at 16; the 8-lane group kernel needs 256 registers and spills at C = 2,
+// 124 B/lane with the split sweeps, which made group chunks 26.0 -> 27.0 ms at 8 sweeps).
 template <int C>
 constexpr bool kGroupChunks = C > 2;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
