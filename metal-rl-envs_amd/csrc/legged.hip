@@ -385,24 +385,33 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     // contact solve, ln_stick, lt_stick, (target - wn) / den_p and (target - wn) / den_m
     // (lanes 4 and up repeat lane 0's). Every broadcast value is the expression the one-lane
     // sweep evaluates, so the impulses are the same bits.
+    // Each lane reads its own coefficients from the group's LDS blocks at a lane-dependent
+    // offset (block (k, l) holds Att, Atn, Ant, Ann; contact k's block holds det, den_p,
+    // den_m and then their float64 reciprocals), and negates by flipping the sign bit: no
+    // per-lane selects, which the compiler had turned into exec-mask branches.
     const bool nrow = (g == 1);
+    const int sel = (g == 2) ? 1 : (g == 3) ? 2 : 0;       // det, den_p, den_m
+    const uint32_t neg = nrow ? 0x80000000u : 0u;
+    const int oA = nrow ? 2 : 0, oB = nrow ? 3 : 1, oQ = nrow ? 1 : 0;  // Ant|Att, Ann|Atn, Atn|Att
     float cA[C][C], cB[C][C], w0x[C], qP[C], qQ[C], qd[C], slipc[C];
     double qr[C];
 #pragma unroll
     for (int k = 0; k < C; ++k) {
 #pragma unroll
       for (int l = 0; l < C; ++l) {
-        cA[k][l] = nrow ? Ant[k][l] : Att[k][l];
-        cB[k][l] = nrow ? Ann[k][l] : Atn[k][l];
+        cA[k][l] = xd[4 * (k * C + l) + oA];
+        cB[k][l] = xd[4 * (k * C + l) + oB];
       }
       w0x[k] = nrow ? w0n[k] : w0t[k];
       // numerators qP * wt + qQ * tw: lane 0 Atn wt + Att tw, which is the reference's
       // Att tw + Atn wt (a rounded sum commutes); lane 1 (-Ann) wt + (-Atn) tw, which is
       // the reference's (-Ann) wt - Atn tw exactly (a - b = a + (-b))
-      qP[k] = nrow ? -blk[k].Ann : blk[k].Atn;
-      qQ[k] = nrow ? -blk[k].Atn : blk[k].Att;
-      qd[k] = (g == 2) ? blk[k].den_p : (g == 3) ? blk[k].den_m : blk[k].det;
-      qr[k] = (g == 2) ? blk[k].rden_p : (g == 3) ? blk[k].rden_m : blk[k].rdet;
+      const float* xb = xd + 4 * (k * C + k);
+      qP[k] = __uint_as_float(__float_as_uint(xb[oB]) ^ neg);
+      qQ[k] = __uint_as_float(__float_as_uint(xb[oQ]) ^ neg);
+      const float* xc = xd + 4 * C * C + 12 * k;
+      qd[k] = xc[sel];
+      qr[k] = *reinterpret_cast<const double*>(xc + 4 + 2 * sel);
       slipc[k] = blk[k].Att * MU + blk[k].Atn;
     }
     for (int it = 0; it < iters; ++it) {
@@ -704,18 +713,29 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
   for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
 #pragma unroll
   for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
-  float hs[(HID + G - 1) / G];
+  constexpr int kUnits = (HID + G - 1) / G;
+  // every weight of the lane's hidden units is loaded before the first use (one memory round
+  // trip); left to itself the scheduler may wait out one round trip per weight
+  float wu[kUnits][1 + OBS];
 #pragma unroll
-  for (int u = 0; u < (HID + G - 1) / G; ++u) {
+  for (int u = 0; u < kUnits; ++u) {
     const int j = g + G * u < HID ? g + G * u : 0;  // lanes past HID recompute unit 0, unused
-    float sj = w[R::b1(j) * kStride];
+    wu[u][0] = w[R::b1(j) * kStride];
 #pragma unroll
-    for (int k = 0; k < OBS; ++k) sj = sj + obs[k] * w[R::w1(k, j) * kStride];
+    for (int k = 0; k < OBS; ++k) wu[u][1 + k] = w[R::w1(k, j) * kStride];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float hs[kUnits];
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u) {
+    float sj = wu[u][0];
+#pragma unroll
+    for (int k = 0; k < OBS; ++k) sj = sj + obs[k] * wu[u][1 + k];
     hs[u] = det_tanh(sj);
   }
   __syncthreads();  // the rows' previous readers are done
 #pragma unroll
-  for (int u = 0; u < (HID + G - 1) / G; ++u)
+  for (int u = 0; u < kUnits; ++u)
     if (g + G * u < HID) xh[g + G * u] = hs[u];
   __syncthreads();
   // lane g sums heads g, g + G, ... over the hidden values in order; a head's HID weights are
@@ -731,6 +751,9 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
     float w2r[HID];
 #pragma unroll
     for (int j = 0; j < HID; ++j) w2r[j] = wh[R::w2(j, o) * kStride];
+    // all HID loads issue before the first use: left to itself the scheduler may pair each
+    // load with its product and wait out one memory round trip per weight
+    __builtin_amdgcn_sched_barrier(0);
     float lo = w[R::b2(o) * kStride];
 #pragma unroll
     for (int j = 0; j < HID; ++j) lo = lo + xh[j] * w2r[j];
