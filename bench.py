@@ -104,8 +104,8 @@ STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k
                      "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
                      "legged4_s8_reference": 16402572}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110170000000, (4, 8): 125700000000, (4, 16): 139940000000,
-                          (2, 4): 40946000000, (2, 8): 42354000000, (2, 16): 49674000000}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110150000000, (4, 8): 125680000000, (4, 16): 139910000000,
+                          (2, 4): 40940000000, (2, 8): 42358000000, (2, 16): 49670000000}
 
 
 def log(msg):
