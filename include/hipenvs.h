@@ -367,6 +367,15 @@ int hipenvs_detmath(const float* x, float* sin_out, float* cos_out, float* tanh_
 int hipenvs_div_recip(const float* a, const float* d, float* q, uint8_t* marked, int64_t n,
                       hipenvs_stream_t stream);
 
+/* For every float32 bit pattern first .. first + count - 1 (within 0 .. 2^32 - 1): the
+ * kernels' square root (float64 reciprocal square root estimate and one Newton step,
+ * rounded to float32) against IEEE sqrtf, and their float64 reciprocal (hardware estimate
+ * and two Newton steps) against IEEE 1.0 / (double)x, bit for bit. Adds the mismatch
+ * counts to counts[0] (square root) and counts[1] (reciprocal), device memory the caller
+ * zeroes. */
+int hipenvs_sqrt_recip_check(uint64_t first, uint64_t count, unsigned long long* counts,
+                             hipenvs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

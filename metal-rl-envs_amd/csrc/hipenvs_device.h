@@ -253,7 +253,36 @@ __device__ __forceinline__ float div_const(float x, double inv_c) { return (floa
 // midpoint, where the product may round either way. DivRecip marks a lane whose quotient
 // came out nonzero subnormal (a compare and a select, no branch); its caller then redoes
 // the computation with IEEE division (DivIEEE), a path these bodies never take in practice.
-__device__ __forceinline__ double recip(float d) { return 1.0 / (double)d; }
+//
+// recip(d) is IEEE 1.0 / (double)d, formed from the hardware float64 reciprocal estimate
+// and two Newton steps, e = 1 - d r, r += r e (each one fused multiply-add): six
+// instructions where the IEEE float64 division takes eleven. For d = +-0, +-inf or NaN the
+// residual is NaN and the estimate (+-inf, +-0, NaN) is the answer. Equal to
+// 1.0 / (double)d bit for bit for all 2^32 float32 d (hipenvs_sqrt_recip_check, run by the
+// GPU tests), so the argument above holds unchanged.
+__device__ __forceinline__ double recip(float d) {
+  const double x = (double)d;
+  const double r0 = __builtin_amdgcn_rcp(x);
+  double e = __builtin_fma(-x, r0, 1.0);
+  double r = __builtin_fma(r0, e, r0);
+  e = __builtin_fma(-x, r, 1.0);
+  r = __builtin_fma(r, e, r);
+  return (e == e) ? r : r0;
+}
+
+// IEEE sqrtf(x), formed in float64 from the hardware reciprocal square root estimate r:
+// g = x r, then one Newton step g += (r / 2)(x - g^2), rounded to float32; +-0 and +inf pass
+// through, negative inputs and NaN give NaN. Nine instructions where the correctly rounded
+// float32 expansion takes about sixteen. Equal to IEEE sqrtf bit for bit (NaN for NaN) for
+// all 2^32 float32 x (hipenvs_sqrt_recip_check, run by the GPU tests).
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const double d = (double)x;
+  const double r = __builtin_amdgcn_rsq(d);
+  const double g = d * r;
+  const double e = __builtin_fma(-g, g, d);
+  const float y = (float)__builtin_fma(0.5 * r, e, g);
+  return __builtin_amdgcn_classf(x, 0x260) ? x : y;  // class bits 5, 6, 9: -0, +0, +inf
+}
 
 struct DivRecip {
   // Per lane, the least (bits << 1) - 2 over the quotients, in uint32 arithmetic: the shift

@@ -225,7 +225,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
 #pragma unroll
       for (int p = 0; p < j; ++p) s = s - L[i][p] * L[j][p];
       if (i == j) {
-        L[i][i] = sqrtf(s);
+        L[i][i] = sqrt_rn(s);
         rL[i] = recip(L[i][i]);
       } else {
         L[i][j] = div(s, L[j][j], rL[j]);

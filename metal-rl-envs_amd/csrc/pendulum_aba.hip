@@ -178,7 +178,7 @@ __device__ __forceinline__ void mass_matrix_accelerations(const float* th, const
       float t = L[i][j];
 #pragma unroll
       for (int p = 0; p < j; ++p) t = t - L[i][p] * L[j][p];
-      L[i][j] = (i == j) ? sqrtf(t) : t / L[j][j];
+      L[i][j] = (i == j) ? sqrt_rn(t) : t / L[j][j];
     }
   }
 #pragma unroll

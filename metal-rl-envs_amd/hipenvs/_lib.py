@@ -25,6 +25,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
 _U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
 _F32 = ctypes.c_float
 
 # name -> argtypes, every entry point of include/hipenvs.h that returns a status int
@@ -35,6 +36,7 @@ SIGNATURES = {
     "hipenvs_sample_actions": [_P, _I64, _I32, _U32, _P],
     "hipenvs_detmath": [_P, _P, _P, _P, _I64, _P],
     "hipenvs_div_recip": [_P, _P, _P, _P, _I64, _P],
+    "hipenvs_sqrt_recip_check": [_U64, _U64, _P, _P],
     "hipenvs_cartpole_es_rollout": [_P, _P, _I64, _I32, _I32, _P, _P],
     "hipenvs_acrobot_reset": [_P, _I64, _U32, _P],
     "hipenvs_acrobot_step": [_P, _P, _U32, _P, _P, _P, _I64, _P],

@@ -62,3 +62,28 @@ def test_div_recip_is_ieee_division(dev):
     # the redo path ran and mattered: exact subnormal midpoints where the product alone is wrong
     wrong = (fast.view(np.uint32) != want.view(np.uint32)) & ~(np.isnan(fast) & np.isnan(want))
     assert wrong.sum() > 100 and marked[wrong].all()
+
+
+@pytest.mark.gpu
+def test_sqrt_and_recip_match_ieee_for_every_float32(dev):
+    """The kernels' square root (float64 reciprocal square root estimate, one Newton step,
+    rounded to float32) and float64 reciprocal (hardware estimate, two Newton steps) against
+    IEEE sqrtf and 1.0 / (double)x, over all 2^32 float32 bit patterns, in 16 launches of
+    2^28. The Cholesky pivots and the shared-reciprocal divisions rest on both."""
+    counts = torch.zeros(2, dtype=torch.int64, device=dev)
+    step = 1 << 28
+    for first in range(0, 1 << 32, step):
+        _lib.call("hipenvs_sqrt_recip_check", first, step, _lib.ptr(counts), _lib.stream_of(dev))
+    sqrt_bad, recip_bad = counts.cpu().tolist()
+    assert (sqrt_bad, recip_bad) == (0, 0)
+
+
+@pytest.mark.gpu
+def test_sqrt_recip_check_argument_bounds(dev):
+    """The check's own arguments: a range past 2^32 is refused, an empty one does nothing."""
+    counts = torch.zeros(2, dtype=torch.int64, device=dev)
+    with pytest.raises(RuntimeError):
+        _lib.call("hipenvs_sqrt_recip_check", (1 << 32) - 4, 8, _lib.ptr(counts), _lib.stream_of(dev))
+    _lib.call("hipenvs_sqrt_recip_check", 0, 0, _lib.ptr(counts), _lib.stream_of(dev))
+    assert counts.cpu().tolist() == [0, 0]
+
