@@ -145,11 +145,12 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
 // the reference's pendulum_metal.py): M_ij = mu_ij cos(th_i - th_j) and
 // rhs_i = -sum_j mu_ij sin(th_i - th_j) om_j^2 - g mu_ii sin th_i (+ torque at the root),
 // with mu_ij = K - max(i, j) and the differences' cos/sin from K cosines and K sines by the
-// addition formulas, then the Cholesky solve of pendulum_np.py:85-107 (IEEE sqrt and
-// division). Sums run in numpy's order: over j for each row, the factor's rows left to right.
-template <int K>
-__device__ __forceinline__ void mass_matrix_accelerations(const float* th, const float* om, float torque,
-                                                          float* acc) {
+// addition formulas, then the Cholesky solve of pendulum_np.py:85-107 (the IEEE square root
+// and quotients, bit for bit). Sums run in numpy's order: over j for each row, the factor's
+// rows left to right.
+template <int K, class Div>
+__device__ __forceinline__ void mass_matrix_accelerations_with(const float* th, const float* om, float torque,
+                                                               float* acc, Div& div) {
   float c[K], s[K], w2[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
@@ -170,7 +171,9 @@ __device__ __forceinline__ void mass_matrix_accelerations(const float* th, const
     y[i] = (-r) - (GRAVITY * (float)(K - i)) * s[i];
   }
   y[0] = y[0] + torque;
-  // L L^T = M in place, then L y' = y and L^T x = y'
+  // L L^T = M in place, then L y' = y and L^T x = y'; every quotient divides by a pivot,
+  // whose float64 reciprocal is formed once
+  double rL[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
 #pragma unroll
@@ -178,7 +181,12 @@ __device__ __forceinline__ void mass_matrix_accelerations(const float* th, const
       float t = L[i][j];
 #pragma unroll
       for (int p = 0; p < j; ++p) t = t - L[i][p] * L[j][p];
-      L[i][j] = (i == j) ? sqrt_rn(t) : t / L[j][j];
+      if (i == j) {
+        L[i][i] = sqrt_rn(t);
+        rL[i] = recip(L[i][i]);
+      } else {
+        L[i][j] = div(t, L[j][j], rL[j]);
+      }
     }
   }
 #pragma unroll
@@ -186,14 +194,28 @@ __device__ __forceinline__ void mass_matrix_accelerations(const float* th, const
     float t = y[i];
 #pragma unroll
     for (int p = 0; p < i; ++p) t = t - L[i][p] * y[p];
-    y[i] = t / L[i][i];
+    y[i] = div(t, L[i][i], rL[i]);
   }
 #pragma unroll
   for (int i = K - 1; i >= 0; --i) {
     float t = y[i];
 #pragma unroll
     for (int p = i + 1; p < K; ++p) t = t - L[p][i] * acc[p];
-    acc[i] = t / L[i][i];
+    acc[i] = div(t, L[i][i], rL[i]);
+  }
+}
+
+// The mass-matrix model's accelerations (pendulum_np.py:69-95). Divisions go through the
+// pivots' shared float64 reciprocals (DivRecip: the IEEE quotient unless it is subnormal);
+// a lane on which a quotient came out subnormal evaluates again with IEEE division.
+template <int K>
+__device__ __forceinline__ void mass_matrix_accelerations(const float* th, const float* om, float torque,
+                                                          float* acc) {
+  DivRecip fast;
+  mass_matrix_accelerations_with<K>(th, om, torque, acc, fast);
+  if (fast.saw_subnormal()) {
+    DivIEEE ieee;
+    mass_matrix_accelerations_with<K>(th, om, torque, acc, ieee);
   }
 }
 
