@@ -47,9 +47,12 @@ __device__ __forceinline__ void own_bias(float w, float x, float y, float& p0, f
   p2 = w * x;
 }
 
-// Absolute angular accelerations acc[K] from absolute angles th[K] and velocities om[K].
-template <int K, int U = K>
-__device__ __forceinline__ void accelerations(const float* th, const float* om, float torque, float* acc) {
+// Absolute angular accelerations acc[K] from absolute angles th[K] and velocities om[K],
+// dividing with Div: a link's eight quotients share its pivot D, whose float64 reciprocal
+// is formed once in each pass.
+template <int K, int U, class Div>
+__device__ __forceinline__ void accelerations_with(const float* th, const float* om, float torque, float* acc,
+                                                   Div& div) {
   float cs[K], sn[K], vw[K], vx[K], vy[K], U0[K], U1[K], U2[K], uu[K];
   // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
   {
@@ -86,15 +89,16 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
       uu[i] = (i == 0 ? torque : 0.0f) - P0;
       if (i == 0) break;
       const float D = A0;
-      const float I0 = A0 - (A0 * A0) / D, I1 = A1 - (A0 * A1) / D, I2 = A2 - (A0 * A2) / D;
-      const float I3 = A3 - (A1 * A1) / D, I4 = A4 - (A1 * A2) / D, I5 = A5 - (A2 * A2) / D;
+      const double rD = recip(D);
+      const float I0 = A0 - div(A0 * A0, D, rD), I1 = A1 - div(A0 * A1, D, rD), I2 = A2 - div(A0 * A2, D, rD);
+      const float I3 = A3 - div(A1 * A1, D, rD), I4 = A4 - div(A1 * A2, D, rD), I5 = A5 - div(A2 * A2, D, rD);
       const float qd = om[i] - om[i - 1];
       const float c1 = qd * vy[i], c2 = (-qd) * vx[i];
       // Ia c with c = (0, c1, c2); the reference adds the exact zero term Ia_j0 * 0 first.
       const float Iac0 = I1 * c1 + I2 * c2;
       const float Iac1 = I3 * c1 + I4 * c2;
       const float Iac2 = I4 * c1 + I5 * c2;
-      const float g = uu[i] / D;
+      const float g = div(uu[i], D, rD);
       const float pa0 = (P0 + Iac0) + A0 * g;
       const float pa1 = (P1 + Iac1) + A1 * g;
       const float pa2 = (P2 + Iac2) + A2 * g;
@@ -131,13 +135,34 @@ __device__ __forceinline__ void accelerations(const float* th, const float* om, 
       const float ap0 = aw;
       const float ap1 = (c * ax + s * xy) + c1;
       const float ap2 = ((-s) * ax + c * xy) + c2;
-      const float qdd = (uu[i] - ((U0[i] * ap0 + U1[i] * ap1) + U2[i] * ap2)) / U0[i];
+      const float qdd = div(uu[i] - ((U0[i] * ap0 + U1[i] * ap1) + U2[i] * ap2), U0[i], recip(U0[i]));
       aw = ap0 + qdd;
       ax = ap1;
       ay = ap2;
       run = run + qdd;
       acc[i] = run;
     }
+  }
+}
+
+// accelerations_with through the pivots' shared float64 reciprocals (DivRecip: the IEEE
+// quotient unless it is subnormal); a lane on which a quotient came out subnormal
+// evaluates again with IEEE division, so the results are IEEE's bit for bit. Semi-implicit
+// Euler at N = 65,536: K = 16 11.98 -> 11.35 us per step; K = 4, at the launch floor, 3.75 ->
+// 3.82 us. Past K = 16 the second copy of the evaluation costs scratch (the K = 32 Euler
+// step spilled 184 B/lane). So K = 5..16 divide this way, the others with IEEE division.
+template <int K, int U = K>
+__device__ __forceinline__ void accelerations(const float* th, const float* om, float torque, float* acc) {
+  if constexpr (K > 4 && K <= 16) {
+    DivRecip fast;
+    accelerations_with<K, U>(th, om, torque, acc, fast);
+    if (fast.saw_subnormal()) {
+      DivIEEE ieee;
+      accelerations_with<K, U>(th, om, torque, acc, ieee);
+    }
+  } else {
+    DivIEEE ieee;
+    accelerations_with<K, U>(th, om, torque, acc, ieee);
   }
 }
 
@@ -207,13 +232,20 @@ __device__ __forceinline__ void mass_matrix_accelerations_with(const float* th, 
 
 // The mass-matrix model's accelerations (pendulum_np.py:69-95). Divisions go through the
 // pivots' shared float64 reciprocals (DivRecip: the IEEE quotient unless it is subnormal);
-// a lane on which a quotient came out subnormal evaluates again with IEEE division.
+// a lane on which a quotient came out subnormal evaluates again with IEEE division. RK4 at
+// N = 65,536: K = 16 55.5 -> 48.4 us per step, K = 8 16.1 -> 15.2, K = 4 6.85 -> 6.63; at
+// K = 2 (3.97 -> 4.17 us) it divides with IEEE division alone.
 template <int K>
 __device__ __forceinline__ void mass_matrix_accelerations(const float* th, const float* om, float torque,
                                                           float* acc) {
-  DivRecip fast;
-  mass_matrix_accelerations_with<K>(th, om, torque, acc, fast);
-  if (fast.saw_subnormal()) {
+  if constexpr (K > 2) {
+    DivRecip fast;
+    mass_matrix_accelerations_with<K>(th, om, torque, acc, fast);
+    if (fast.saw_subnormal()) {
+      DivIEEE ieee;
+      mass_matrix_accelerations_with<K>(th, om, torque, acc, ieee);
+    }
+  } else {
     DivIEEE ieee;
     mass_matrix_accelerations_with<K>(th, om, torque, acc, ieee);
   }
