@@ -421,6 +421,106 @@ struct RowBuffer {
   }
 };
 
+// The staged kernel's first pass (pendulum_aba_np.py:36-50): link velocities in link frames
+// and joint rates from the inputs (read kOutwardAhead links ahead of their use), the joints'
+// sin and cos into the LDS rows.
+template <int K>
+__device__ __forceinline__ void staged_outward(const RowBuffer& in, float* sn_l, float* cs_l, float (&vw)[K],
+                                               float (&vx)[K], float (&vy)[K], float (&qdv)[K]) {
+  float w = 0.0f, x = 0.0f, y = 0.0f, th_prev = 0.0f, om_prev = 0.0f;
+  float th0[K], om0[K];  // the inputs, read kOutwardAhead links ahead of their use
+#pragma unroll
+  for (int j = 0; j < K && j < kOutwardAhead; ++j) {
+    th0[j] = in.load(j);
+    om0[j] = in.load(K + j);
+  }
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (i + kOutwardAhead < K) {
+      th0[i + kOutwardAhead] = in.load(i + kOutwardAhead);
+      om0[i + kOutwardAhead] = in.load(K + i + kOutwardAhead);
+    }
+    const float th_i = th0[i], om_i = om0[i];
+    const float q = (i == 0) ? th_i : th_i - th_prev;
+    const float qd = (i == 0) ? om_i : om_i - om_prev;
+    float sn, cs;
+    det_sincos(q, &sn, &cs);
+    sn_l[i * kBlock] = sn;
+    cs_l[i * kBlock] = cs;
+    const float xy = (i == 0) ? (y + w * 0.0f) : (y + w);
+    const float nw = w + qd;
+    const float nx = cs * x + sn * xy;
+    const float ny = (-sn) * x + cs * xy;
+    vw[i] = nw;
+    vx[i] = nx;
+    vy[i] = ny;
+    qdv[i] = qd;
+    w = nw;
+    x = nx;
+    y = ny;
+    th_prev = th_i;
+    om_prev = om_i;
+  }
+}
+
+// The staged kernel's inward pass (pendulum_aba_np.py:51-82): articulated inertia and bias
+// folded into the parent, writing U and u per link; a link's seven quotients divide by its
+// pivot D through Div. cv, sv are rotating registers for the LDS rows of cos and sin.
+template <int K, class Div>
+__device__ __forceinline__ void staged_inward(const float (&vw)[K], const float (&vx)[K], const float (&vy)[K],
+                                              const float (&qdv)[K], const float* cs_l, const float* sn_l,
+                                              float tq, float (&U0)[K], float (&U1)[K], float (&U2)[K],
+                                              float (&uu)[K], float (&cv)[K], float (&sv)[K], Div& div) {
+  float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
+  float P0, P1, P2;
+  own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
+#pragma unroll
+  for (int j = K - 1; j >= 1 && j > K - 1 - kStageLinks; --j) {
+    cv[j] = cs_l[j * kBlock];
+    sv[j] = sn_l[j * kBlock];
+  }
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) {
+    U0[i] = A0;
+    U1[i] = A1;
+    U2[i] = A2;
+    uu[i] = (i == 0 ? tq : 0.0f) - P0;
+    if (i == 0) break;
+    if (i - kStageLinks >= 1) {
+      cv[i - kStageLinks] = cs_l[(i - kStageLinks) * kBlock];
+      sv[i - kStageLinks] = sn_l[(i - kStageLinks) * kBlock];
+    }
+    const float D = A0;
+    const double rD = recip(D);
+    const float I0 = A0 - div(A0 * A0, D, rD), I1 = A1 - div(A0 * A1, D, rD), I2 = A2 - div(A0 * A2, D, rD);
+    const float I3 = A3 - div(A1 * A1, D, rD), I4 = A4 - div(A1 * A2, D, rD), I5 = A5 - div(A2 * A2, D, rD);
+    const float c1 = qdv[i] * vy[i], c2 = (-qdv[i]) * vx[i];
+    const float Iac0 = I1 * c1 + I2 * c2;
+    const float Iac1 = I3 * c1 + I4 * c2;
+    const float Iac2 = I4 * c1 + I5 * c2;
+    const float g = div(uu[i], D, rD);
+    const float pa0 = (P0 + Iac0) + A0 * g;
+    const float pa1 = (P1 + Iac1) + A1 * g;
+    const float pa2 = (P2 + Iac2) + A2 * g;
+    const float c = cv[i], s = sv[i];
+    const float B00 = (I0 + I1 * s) + I2 * c, B01 = I1 * c - I2 * s, B02 = I1 * s + I2 * c;
+    const float B10 = (I1 + I3 * s) + I4 * c, B11 = I3 * c - I4 * s, B12 = I3 * s + I4 * c;
+    const float B20 = (I2 + I4 * s) + I5 * c, B21 = I4 * c - I5 * s, B22 = I4 * s + I5 * c;
+    A0 = 1.0f + ((B00 + s * B10) + c * B20);
+    A1 = (B01 + s * B11) + c * B21;
+    A2 = 1.0f + ((B02 + s * B12) + c * B22);
+    A3 = 1.0f + (c * B11 - s * B21);
+    A4 = c * B12 - s * B22;
+    A5 = 1.0f + (s * B12 + c * B22);
+    float pp0, pp1, pp2;
+    own_bias(vw[i - 1], vx[i - 1], vy[i - 1], pp0, pp1, pp2);
+    P0 = ((pp0 + pa0) + s * pa1) + c * pa2;
+    P1 = (pp1 + c * pa1) - s * pa2;
+    P2 = (pp2 + s * pa1) + c * pa2;
+    if ((i & (kStageLinks - 1)) == 0) asm volatile("" ::: "memory");  // LDS reads kStageLinks links ahead at most
+  }
+}
+
 // The Euler step for long chains with the per-link state staged by lifetime. At K = 64 the
 // step of the generic form holds the input angles and velocities and every per-link array
 // for the whole step, about 790 floats per lane, and spills past the 512 registers. Here:
@@ -449,95 +549,24 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
                                 : uniform_pm(pcg_hash(env_hash(seed, (uint32_t)e) + kTorqueOffset), 1.0f);
   float vw[K], vx[K], vy[K], qdv[K], U0[K], U1[K], U2[K], uu[K];
   const RowBuffer in(state, 2 * K, n, e);
-  // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
-  {
-    float w = 0.0f, x = 0.0f, y = 0.0f, th_prev = 0.0f, om_prev = 0.0f;
-    float th0[K], om0[K];  // the inputs, read kOutwardAhead links ahead of their use
-#pragma unroll
-    for (int j = 0; j < K && j < kOutwardAhead; ++j) {
-      th0[j] = in.load(j);
-      om0[j] = in.load(K + j);
-    }
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      if (i + kOutwardAhead < K) {
-        th0[i + kOutwardAhead] = in.load(i + kOutwardAhead);
-        om0[i + kOutwardAhead] = in.load(K + i + kOutwardAhead);
-      }
-      const float th_i = th0[i], om_i = om0[i];
-      const float q = (i == 0) ? th_i : th_i - th_prev;
-      const float qd = (i == 0) ? om_i : om_i - om_prev;
-      float sn, cs;
-      det_sincos(q, &sn, &cs);
-      sn_l[i * kBlock] = sn;
-      cs_l[i * kBlock] = cs;
-      const float xy = (i == 0) ? (y + w * 0.0f) : (y + w);
-      const float nw = w + qd;
-      const float nx = cs * x + sn * xy;
-      const float ny = (-sn) * x + cs * xy;
-      vw[i] = nw;
-      vx[i] = nx;
-      vy[i] = ny;
-      qdv[i] = qd;
-      w = nw;
-      x = nx;
-      y = ny;
-      th_prev = th_i;
-      om_prev = om_i;
-    }
-  }
+  staged_outward<K>(in, sn_l, cs_l, vw, vx, vy, qdv);
   asm volatile("" ::: "memory");  // each pass reads its LDS rows in its own order, not hoisted into the last
   // inward: articulated inertia and bias folded into the parent (pendulum_aba_np.py:51-82)
   // Each pass below issues its reads kStageLinks links ahead of their use (rotating
   // registers), so their latency overlaps the links in between.
   float cv[K], sv[K];
   {
-    float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
-    float P0, P1, P2;
-    own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
-#pragma unroll
-    for (int j = K - 1; j >= 1 && j > K - 1 - kStageLinks; --j) {
-      cv[j] = cs_l[j * kBlock];
-      sv[j] = sn_l[j * kBlock];
-    }
-#pragma unroll
-    for (int i = K - 1; i >= 0; --i) {
-      U0[i] = A0;
-      U1[i] = A1;
-      U2[i] = A2;
-      uu[i] = (i == 0 ? tq : 0.0f) - P0;
-      if (i == 0) break;
-      if (i - kStageLinks >= 1) {
-        cv[i - kStageLinks] = cs_l[(i - kStageLinks) * kBlock];
-        sv[i - kStageLinks] = sn_l[(i - kStageLinks) * kBlock];
-      }
-      const float D = A0;
-      const float I0 = A0 - (A0 * A0) / D, I1 = A1 - (A0 * A1) / D, I2 = A2 - (A0 * A2) / D;
-      const float I3 = A3 - (A1 * A1) / D, I4 = A4 - (A1 * A2) / D, I5 = A5 - (A2 * A2) / D;
-      const float c1 = qdv[i] * vy[i], c2 = (-qdv[i]) * vx[i];
-      const float Iac0 = I1 * c1 + I2 * c2;
-      const float Iac1 = I3 * c1 + I4 * c2;
-      const float Iac2 = I4 * c1 + I5 * c2;
-      const float g = uu[i] / D;
-      const float pa0 = (P0 + Iac0) + A0 * g;
-      const float pa1 = (P1 + Iac1) + A1 * g;
-      const float pa2 = (P2 + Iac2) + A2 * g;
-      const float c = cv[i], s = sv[i];
-      const float B00 = (I0 + I1 * s) + I2 * c, B01 = I1 * c - I2 * s, B02 = I1 * s + I2 * c;
-      const float B10 = (I1 + I3 * s) + I4 * c, B11 = I3 * c - I4 * s, B12 = I3 * s + I4 * c;
-      const float B20 = (I2 + I4 * s) + I5 * c, B21 = I4 * c - I5 * s, B22 = I4 * s + I5 * c;
-      A0 = 1.0f + ((B00 + s * B10) + c * B20);
-      A1 = (B01 + s * B11) + c * B21;
-      A2 = 1.0f + ((B02 + s * B12) + c * B22);
-      A3 = 1.0f + (c * B11 - s * B21);
-      A4 = c * B12 - s * B22;
-      A5 = 1.0f + (s * B12 + c * B22);
-      float pp0, pp1, pp2;
-      own_bias(vw[i - 1], vx[i - 1], vy[i - 1], pp0, pp1, pp2);
-      P0 = ((pp0 + pa0) + s * pa1) + c * pa2;
-      P1 = (pp1 + c * pa1) - s * pa2;
-      P2 = (pp2 + s * pa1) + c * pa2;
-      if ((i & (kStageLinks - 1)) == 0) asm volatile("" ::: "memory");  // LDS reads kStageLinks links ahead at most
+    // through the pivots' shared float64 reciprocals; a lane on which a quotient came out
+    // subnormal runs the first two passes again, with IEEE division (nothing is stored
+    // before the last pass and the inputs are only read, so the redo starts from them and
+    // no first-pass value has to outlive the first attempt)
+    DivRecip fast;
+    staged_inward<K>(vw, vx, vy, qdv, cs_l, sn_l, tq, U0, U1, U2, uu, cv, sv, fast);
+    if (fast.saw_subnormal()) {
+      staged_outward<K>(in, sn_l, cs_l, vw, vx, vy, qdv);
+      asm volatile("" ::: "memory");
+      DivIEEE ieee;
+      staged_inward<K>(vw, vx, vy, qdv, cs_l, sn_l, tq, U0, U1, U2, uu, cv, sv, ieee);
     }
   }
   asm volatile("" ::: "memory");
