@@ -99,13 +99,13 @@ CARTPOLE_BYTES = 41
 # Tables and commands: profiles/cartpole_step_n262144.md, profiles/aba_euler_n65536.md,
 # profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
-ABA_TRAFFIC = {4: 4654925, 16: 17652919, 64: 100206816}
+ABA_TRAFFIC = {4: 4653834, 16: 17593455, 64: 99827206}
 STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k8": 9770478,
                      "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
                      "legged4_s8_reference": 16402572}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110150000000, (4, 8): 125680000000, (4, 16): 139910000000,
-                          (2, 4): 40940000000, (2, 8): 42358000000, (2, 16): 49670000000}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110160000000, (4, 8): 125690000000, (4, 16): 139900000000,
+                          (2, 4): 40933000000, (2, 8): 42362000000, (2, 16): 49676000000}
 
 
 def log(msg):
