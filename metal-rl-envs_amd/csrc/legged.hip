@@ -632,12 +632,6 @@ inline int32_t first_chunk_steps(int32_t chunk_steps) {
   return kFirstChunkSteps<C> > 0 && kFirstChunkSteps<C> < chunk_steps ? kFirstChunkSteps<C> : chunk_steps;
 }
 
-// POLICY_UNROLL hidden units per policy loop iteration bounds how many of the member's
-// weight loads are in flight at once.
-#ifndef POLICY_UNROLL
-#define POLICY_UNROLL 4
-#endif
-
 // Rows of the policy weights. FlatRows is es.unflatten's layout (es.py:152-164): w1 (OBS, HID)
 // row-major, b1 (HID), w2 (HID, OUT) row-major, b2 (OUT), the layout callers pass in.
 // UnitRows is the compacted sets' layout: hidden unit j's bias, its OBS input weights and
@@ -680,14 +674,37 @@ __device__ __forceinline__ void policy_torques(const float* __restrict__ w, int6
   float logit[OUT];
 #pragma unroll
   for (int o = 0; o < OUT; ++o) logit[o] = w[R::b2(o) * stride];
-#pragma unroll POLICY_UNROLL
-  for (int j = 0; j < HID; ++j) {
-    float s = w[R::b1(j) * stride];
+  // kBatch hidden units at a time: their weights are loaded before the first use and a
+  // scheduling barrier keeps them there, so the loads of a batch share one memory round
+  // trip whatever the scheduler would otherwise interleave (left to itself it has waited on
+  // the biped's weights one at a time). Two units at C = 4 keep two waves per SIMD (236
+  // registers; four-unit batches took 318); four at C <= 2 (169 registers) match the
+  // biped's rollout before this form (ES rollout 25.0 ms at 8 sweeps; two units: 25.5).
+  constexpr int kWant = C <= 2 ? 4 : 2;
+  constexpr int kBatch = kWant <= HID ? kWant : HID;
+  static_assert(HID % kBatch == 0, "whole batches of hidden units");
+#pragma unroll 2
+  for (int j0 = 0; j0 < HID; j0 += kBatch) {
+    float wb[kBatch][1 + OBS + OUT];
 #pragma unroll
-    for (int k = 0; k < OBS; ++k) s = s + obs[k] * w[R::w1(k, j) * stride];
-    const float hj = det_tanh(s);
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u;
+      wb[u][0] = w[R::b1(j) * stride];
 #pragma unroll
-    for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w[R::w2(j, o) * stride];
+      for (int k = 0; k < OBS; ++k) wb[u][1 + k] = w[R::w1(k, j) * stride];
+#pragma unroll
+      for (int o = 0; o < OUT; ++o) wb[u][1 + OBS + o] = w[R::w2(j, o) * stride];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      float s = wb[u][0];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) s = s + obs[k] * wb[u][1 + k];
+      const float hj = det_tanh(s);
+#pragma unroll
+      for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * wb[u][1 + OBS + o];
+    }
   }
 #pragma unroll
   for (int leg = 0; leg < C; ++leg) {
