@@ -191,14 +191,18 @@ __device__ __forceinline__ float half_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(lo, x, 0x150 + 8 + L, 0xF, 0xC, false));
 }
 
-// Lane L of each G-lane group (G = 8 or 16) on every lane of that group.
+// Lane L of each G-lane group (G = 4, 8 or 16) on every lane of that group; a 4-lane group
+// is a DPP quad, broadcast by one quad_perm move.
 template <int G, int L>
 __device__ __forceinline__ float lane_bcast(float v) {
-  static_assert(G == 8 || G == 16, "groups of 8 or 16 lanes");
+  static_assert(G == 4 || G == 8 || G == 16, "groups of 4, 8 or 16 lanes");
   if constexpr (G == 16) {
     return group_bcast<L>(v);
-  } else {
+  } else if constexpr (G == 8) {
     return half_bcast<L>(v);
+  } else {
+    static_assert(L >= 0 && L < 4, "a lane of the quad");
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), L * 0x55, 0xF, 0xF, false));
   }
 }
 

@@ -154,7 +154,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
                                         int g = 0, float* xd = nullptr) {
   constexpr int N = 3 + C;
   float ca[C], sa[C], dx[C], dy[C], depth[C], r2[C];
-  if constexpr (kGroup == 8 || kGroup == 16) {
+  if constexpr (kGroup >= 4 && kGroup >= C) {
     // lane g < C evaluates foot g's sin and cos, shared by DPP broadcast within the group
     static_assert(C <= kGroup, "one lane per foot");
     float a = q[2] + q[3];
@@ -378,7 +378,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       blk[k] = contact_block(Att[k][k], Atn[k][k], Ann[k][k]);
     }
   }
-  if constexpr (kGroup == 8 || kGroup == 16) {
+  if constexpr (kGroup >= 4) {
     // The member's lanes split each contact's independent work and share the results by
     // DPP broadcast: lane 1 forms the normal coupling sum and every other lane the tangential
     // one (each with its own coefficient rows), and lanes 0-3 form the four quotients of the
@@ -491,7 +491,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         MiJn[k][i] = xs[((C + k) * N + i) * 64];
       }
     }
-  } else if constexpr ((kGroup == 8 || kGroup == 16) && !kHopperSum) {
+  } else if constexpr (kGroup >= 3 + C && !kHopperSum) {
     // lane i < N forms velocity i (its sum over the contacts in the same order as below,
     // from its own column of the solved rows) and the DPP broadcast gives it to the group
     static_assert(3 + C <= kGroup, "one lane per velocity");
@@ -1085,14 +1085,16 @@ constexpr int kGroupLanes = 16;
 #endif
 // Above the tail's bound and up to this many survivors per CU, a chunk runs in the group form
 // (rollout_group_chunk_kernel) instead of one member per lane, with LEGGED_GROUP_CHUNK_LANES
-// lanes per member: 8 lanes and up to 48 per CU (one or two 8-member waves per SIMD, 236
-// registers) beat 16 lanes up to 32 per CU (ES rollout at N = 262,144: 57.2 -> 56.3 ms at 8
-// sweeps, 79.0 -> 77.5 ms at 16); 64 per CU was the same as 48, 32 in between.
+// lanes per member. With the split Gauss-Seidel sweeps (a 4-lane group broadcasts with one
+// DPP quad move), 4 lanes and up to 64 per CU at one 16-member wave per SIMD (256 + 107
+// registers; at two waves it spilled 444 B/lane) beat 8 lanes up to 48 per CU at one or two
+// waves (ES rollout at N = 262,144, 8 sweeps: 44.5 -> 43.7 ms). Before those sweeps, 8 lanes
+// had beaten 16 (57.2 -> 56.3 ms) and a spilling 4-lane form (56.0 against 50.0 ms).
 #ifndef LEGGED_GROUP_CHUNK_MEMBERS_PER_CU
-#define LEGGED_GROUP_CHUNK_MEMBERS_PER_CU 48
+#define LEGGED_GROUP_CHUNK_MEMBERS_PER_CU 64
 #endif
 #ifndef LEGGED_GROUP_CHUNK_LANES
-#define LEGGED_GROUP_CHUNK_LANES 8
+#define LEGGED_GROUP_CHUNK_LANES 4
 #endif
 constexpr int kChunkGroupLanes = LEGGED_GROUP_CHUNK_LANES;
 constexpr int kGroupMembers = 64 / kGroupLanes;
@@ -1127,7 +1129,7 @@ __device__ __forceinline__ void rollout_group(const Packed& src, const Packed& d
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   constexpr int D = OBS * HID + HID + HID * OUT + OUT;
   constexpr int M = 64 / G;  // members per single-wave workgroup
-  static_assert(G == 8 || G == 16, "groups of 8 or 16 lanes");
+  static_assert(G == 4 || G == 8 || G == 16, "groups of 4, 8 or 16 lanes");
   const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
   float* xs = xs_all + mloc * (2 * C + 1) * 8;
   float* xd = xd_all + mloc * kBlockFloats<C>;
@@ -1238,7 +1240,7 @@ __global__ __launch_bounds__(64, kTailWaves<C>) void rollout_tail_kernel(Packed 
 // The group form for one chunk, G lanes per member, when the set holds more than lo and at
 // most hi members (a wave or two per SIMD): the survivors go to dst as after a one-lane chunk.
 template <int C, int HID, int G>
-__global__ __launch_bounds__(64, 2) void rollout_group_chunk_kernel(Packed src, Packed dst, int64_t cap,
+__global__ __launch_bounds__(64, G >= 8 ? 2 : 1) void rollout_group_chunk_kernel(Packed src, Packed dst, int64_t cap,
                                                                     int32_t chunk_steps, int32_t horizon, int iters,
                                                                     float alive_bonus, float fall, float gate,
                                                                     float assist, float assist_damping,

@@ -160,19 +160,20 @@ def test_group_tail_equals_static(dev, c, hidden, iters):
         assert ss.max().item() > 8  # members outlived the first chunk
 
 
-@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (2, 32, 8), (4, 64, 8), (2, 64, 4), (4, 64, 16),
-                                            (4, 4, 8), (4, 32, 8)])
-def test_group_chunk_equals_static(dev, c, hidden, iters):
-    """Populations above the group tail's bound (16 members per CU at C = 4, 32 at C <= 2,
-    where the tail runs two waves per SIMD) and within 48 per CU. At C = 4 later chunks run
-    in the group form (8 lanes per member: two solves, two Delassus blocks and up to two
-    heads per lane), at C <= 2 one member per lane; either appends its survivors until the
-    count falls to the tail's bound: member for member equal to the one-lane kernel."""
+@pytest.mark.parametrize("c,hidden,iters,above", [(1, 4, 8, 8), (2, 32, 8, 8), (4, 64, 8, 8), (2, 64, 4, 8),
+                                                  (4, 64, 16, 8), (4, 4, 8, 8), (4, 32, 8, 8), (4, 64, 8, 44)])
+def test_group_chunk_equals_static(dev, c, hidden, iters, above):
+    """Populations `above` members per CU over the group tail's bound (16 per CU at C = 4, 32
+    at C <= 2, where the tail runs two waves per SIMD), within 64 per CU. At C = 4 later
+    chunks run in the group form (4 lanes per member: three solves, four Delassus blocks and
+    three heads per lane, the Gauss-Seidel sweeps split over the quad), at C <= 2 one member
+    per lane; either appends its survivors until the count falls to the tail's bound: member
+    for member equal to the one-lane kernel."""
     from hipenvs import legged, legged_rollout
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     tail_per_cu = 16 if c == 4 else 32
-    p, horizon = (tail_per_cu + 8) * cus, 60
+    p, horizon = (tail_per_cu + above) * cus, 60
     state = legged.Legged(c).reset(p, seed=6, device=dev)
     past_first = 0
     for assist, scale in ((0.0, 0.3), (20.0, 0.0)):
