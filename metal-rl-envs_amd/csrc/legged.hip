@@ -1107,12 +1107,12 @@ constexpr int kGroupMembers = 64 / kGroupLanes;
 template <int C>
 constexpr int kTailWaves = C <= 2 ? 2 : 1;
 // Whether chunks between the tail's bound and LEGGED_GROUP_CHUNK_MEMBERS_PER_CU run in the
-// group form. At C <= 2 the tail already takes over at 32 per CU, and one member per lane
-// down to there was faster (biped ES rollout at N = 262,144: 28.0 -> 27.5 ms at 8 sweeps,
-// 40.2 -> 38.2 ms at 16; the 8-lane group kernel needs 256 registers and spills at C = 2,
-// 124 B/lane with the split sweeps, which made group chunks 26.0 -> 27.0 ms at 8 sweeps).
+// group form. At C <= 2 the tail already takes over at 32 per CU; with 4-lane groups at one
+// wave per SIMD the biped's group chunks between 32 and 64 per CU also pay (biped ES rollout
+// at N = 262,144: 20.2 -> 19.7, 24.9 -> 24.1 and 35.2 -> 33.0 ms at 4, 8, 16 sweeps; the
+// earlier 8-lane groups spilled at C = 2 and were slower than one member per lane).
 template <int C>
-constexpr bool kGroupChunks = C > 2;
+constexpr bool kGroupChunks = true;
 // LDS floats per member for the group substep's Delassus and contact blocks (xd)
 template <int C>
 constexpr int kBlockFloats = 4 * C * C + 12 * C;

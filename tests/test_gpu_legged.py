@@ -161,18 +161,18 @@ def test_group_tail_equals_static(dev, c, hidden, iters):
 
 
 @pytest.mark.parametrize("c,hidden,iters,above", [(1, 4, 8, 8), (2, 32, 8, 8), (4, 64, 8, 8), (2, 64, 4, 8),
-                                                  (4, 64, 16, 8), (4, 4, 8, 8), (4, 32, 8, 8), (4, 64, 8, 44)])
+                                                  (4, 64, 16, 8), (4, 4, 8, 8), (4, 32, 8, 8), (4, 64, 8, 44),
+                                                  (2, 64, 8, 28)])
 def test_group_chunk_equals_static(dev, c, hidden, iters, above):
     """Populations `above` members per CU over the group tail's bound (16 per CU at C = 4, 32
-    at C <= 2, where the tail runs two waves per SIMD), within 64 per CU. At C = 4 later
-    chunks run in the group form (4 lanes per member: three solves, four Delassus blocks and
-    three heads per lane, the Gauss-Seidel sweeps split over the quad), at C <= 2 one member
-    per lane; either appends its survivors until the count falls to the tail's bound: member
-    for member equal to the one-lane kernel."""
+    at C <= 2, where the tail runs two waves per SIMD), within 64 per CU. Later chunks run in
+    the group form (4 lanes per member: the solves, Delassus blocks and heads spread over the
+    quad, the Gauss-Seidel sweeps split over it) and append their survivors until the count
+    falls to the tail's bound: member for member equal to the one-lane kernel."""
     from hipenvs import legged, legged_rollout
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    tail_per_cu = 16 if c == 4 else 32
+    tail_per_cu = 16 if c > 2 else 32
     p, horizon = (tail_per_cu + above) * cus, 60
     state = legged.Legged(c).reset(p, seed=6, device=dev)
     past_first = 0
