@@ -104,8 +104,8 @@ STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k
                      "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
                      "legged4_s8_reference": 16402572}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 110160000000, (4, 8): 125690000000, (4, 16): 139900000000,
-                          (2, 4): 40933000000, (2, 8): 42362000000, (2, 16): 49676000000}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 103070000000, (4, 8): 116230000000, (4, 16): 125450000000,
+                          (2, 4): 46088000000, (2, 8): 49064000000, (2, 16): 65938000000}
 
 
 def log(msg):
