@@ -99,10 +99,10 @@ CARTPOLE_BYTES = 41
 # Tables and commands: profiles/cartpole_step_n262144.md, profiles/aba_euler_n65536.md,
 # profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
-ABA_TRAFFIC = {4: 4653834, 16: 17593455, 64: 99827206}
-STEP_BODY_TRAFFIC = {"pendulum_k2": 2827122, "pendulum_k4": 5094167, "pendulum_k8": 9770478,
-                     "pendulum_k16": 19924955, "hopper": 4884231, "acrobot": 10912296, "legged4_s8": 8232530,
-                     "legged4_s8_reference": 16402572}
+ABA_TRAFFIC = {4: 4649746, 16: 17437438, 64: 99818014}
+STEP_BODY_TRAFFIC = {"pendulum_k2": 2833253, "pendulum_k4": 5104345, "pendulum_k8": 9586116,
+                     "pendulum_k16": 19185779, "hopper": 4889324, "acrobot": 10906005, "legged4_s8": 8227360,
+                     "legged4_s8_reference": 16402468}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
 LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 103070000000, (4, 8): 116230000000, (4, 16): 125450000000,
                           (2, 4): 46088000000, (2, 8): 49064000000, (2, 16): 65938000000}

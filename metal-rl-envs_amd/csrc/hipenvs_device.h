@@ -169,6 +169,30 @@ __device__ __forceinline__ void det_sincos_near_zero(float x, float* sin_out, fl
   }
 }
 
+// Whether every active lane of the wave has |x[i]| <= 0.78 for each of its K values (NaN
+// counts as far): then det_sincos(x[i]) equals sincos_poly(x[i]) for all of them, for the
+// reason given at det_sincos_near_zero. One vote for K arguments; a chain near rest (the
+// pendulums' hanging equilibrium) passes it.
+template <int K>
+__device__ __forceinline__ bool wave_near_zero(const float* x) {
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < K; ++i) ok &= fabsf(x[i]) <= 0.78f;
+  return __all(ok);
+}
+
+// det_sincos of K arguments; the polynomial alone when the wave's vote allows it.
+template <int K>
+__device__ __forceinline__ void det_sincos_all(const float* x, float* sin_out, float* cos_out) {
+  if (wave_near_zero<K>(x)) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) sincos_poly(x[i], &sin_out[i], &cos_out[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) det_sincos(x[i], &sin_out[i], &cos_out[i]);
+  }
+}
+
 // Lane L's value of each 16-lane row of the wave, on every lane of that row (DPP
 // row_newbcast:L): how a 16-lane group shares a value one of its lanes computed. Every lane
 // of every row is written, so the destination needs no prior value (mov_dpp, not update_dpp

@@ -54,15 +54,20 @@ template <int K, int U, class Div>
 __device__ __forceinline__ void accelerations_with(const float* th, const float* om, float torque, float* acc,
                                                    Div& div) {
   float cs[K], sn[K], vw[K], vx[K], vy[K], U0[K], U1[K], U2[K], uu[K];
+  // the joints' sin and cos, by one wave vote for all K joint angles
+  {
+    float q[K];
+#pragma unroll U
+    for (int i = 0; i < K; ++i) q[i] = (i == 0) ? th[0] : th[i] - th[i > 0 ? i - 1 : 0];
+    det_sincos_all<K>(q, sn, cs);
+  }
   // outward: link velocities in link frames (pendulum_aba_np.py:36-50)
   {
     float w = 0.0f, x = 0.0f, y = 0.0f;
 #pragma unroll U
     for (int i = 0; i < K; ++i) {
       const int im = i > 0 ? i - 1 : 0;
-      const float q = (i == 0) ? th[0] : th[i] - th[im];
       const float qd = (i == 0) ? om[0] : om[i] - om[im];
-      det_sincos(q, &sn[i], &cs[i]);
       const float xy = (i == 0) ? (y + w * 0.0f) : (y + w);
       const float nw = w + qd;
       const float nx = cs[i] * x + sn[i] * xy;
@@ -177,11 +182,9 @@ template <int K, class Div>
 __device__ __forceinline__ void mass_matrix_accelerations_with(const float* th, const float* om, float torque,
                                                                float* acc, Div& div) {
   float c[K], s[K], w2[K];
+  det_sincos_all<K>(th, s, c);
 #pragma unroll
-  for (int i = 0; i < K; ++i) {
-    det_sincos(th[i], &s[i], &c[i]);
-    w2[i] = om[i] * om[i];
-  }
+  for (int i = 0; i < K; ++i) w2[i] = om[i] * om[i];
   float L[K][K], y[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
@@ -255,8 +258,17 @@ __device__ __forceinline__ void mass_matrix_accelerations(const float* th, const
 template <int K, int U = K>
 __device__ __forceinline__ bool terminal(const float* th) {
   float s = 0.0f;
+  if (wave_near_zero<K>(th)) {
 #pragma unroll U
-  for (int i = 0; i < K; ++i) s = (i == 0) ? det_cos(th[0]) : s + det_cos(th[i]);
+    for (int i = 0; i < K; ++i) {
+      float sn, cs;
+      sincos_poly(th[i], &sn, &cs);
+      s = (i == 0) ? cs : s + cs;
+    }
+  } else {
+#pragma unroll U
+    for (int i = 0; i < K; ++i) s = (i == 0) ? det_cos(th[0]) : s + det_cos(th[i]);
+  }
   return -s > (float)K * 0.5f;
 }
 

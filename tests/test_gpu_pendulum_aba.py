@@ -116,3 +116,56 @@ def test_k64_euler_full_size_with_terminations(dev):
     np.testing.assert_array_equal(to_np(done), edone)
     np.testing.assert_array_equal(to_np(rew), erew)
     np.testing.assert_array_equal(to_np(ns), ens)
+
+
+def near_rest_states(k, seed):
+    """Angles U[-0.38, 0.38] (every joint angle and every angle within 0.78 of zero), zero
+    velocities, in six waves of 64 envs: waves 0 and 1 stay within the bound (wave 1 with one
+    angle at 0.78 exactly), wave 2 has one root angle a float above 0.78, wave 3 one link at
+    3.0, wave 4 one negative zero, wave 5 one link at -0.8."""
+    r = np.random.default_rng(seed)
+    n = 6 * 64
+    s = np.zeros((2 * k, n), np.float32)
+    s[:k] = r.uniform(-0.38, 0.38, (k, n)).astype(np.float32)
+    s[0, 64 + 17] = np.float32(0.78)
+    s[0, 128 + 5] = np.nextafter(np.float32(0.78), np.float32(1.0))
+    s[k - 1, 192 + 40] = np.float32(3.0)
+    s[0, 256 + 9] = np.float32(-0.0)
+    s[k // 2, 320 + 63] = np.float32(-0.8)
+    return s
+
+
+@pytest.mark.parametrize("k", [4, 16, 32, 64])
+def test_near_rest_waves_match_oracle(dev, k):
+    """A wave whose angles all lie within 0.78 of zero takes the sin/cos polynomial without
+    the range reduction; a wave with one angle outside takes the full reduction. Both give
+    the oracle's bits: accelerations, the Euler step (with its termination cosines) and the
+    RK4 step of the articulated-body model, and the mass-matrix model's step."""
+    from hipenvs import pendulum, pendulum_aba
+
+    state = near_rest_states(k, seed=300 + k)
+    n = state.shape[1]
+    s_dev = torch.from_numpy(state).to(dev)
+    torque = rng.torque_uniform(5, n)
+    t_dev = torch.from_numpy(torque).to(dev)
+    p = pendulum_aba.Pendulum(k)
+    np.testing.assert_array_equal(to_np(p.accelerations(s_dev, t_dev)),
+                                  oaba.aba_accelerations(state[:k], state[k:], torque, k))
+    p.reseed(2)
+    ns, rew, done = p.step_euler(s_dev, t_dev)
+    ens, erew, edone = oaba.Pendulum(k).step_euler(state, torque, seed=3)
+    np.testing.assert_array_equal(to_np(ns), ens)
+    np.testing.assert_array_equal(to_np(done), edone)
+    action = np.random.default_rng(k).integers(0, 3, n)
+    p.reseed(4)
+    ns, rew, done = p.step(s_dev, torch.from_numpy(action.astype(np.int32)).to(dev))
+    ens, erew, edone = oaba.Pendulum(k).step(state, action, seed=5)
+    np.testing.assert_array_equal(to_np(ns), ens)
+    np.testing.assert_array_equal(to_np(done), edone)
+    if k <= 16:
+        env = pendulum.Pendulum(k)
+        env.reseed(6)
+        nxt, rew, done = env.step(s_dev, torch.from_numpy(action.astype(np.int32)).to(dev))
+        e_next, e_rew, e_done = mm.Pendulum(k).step(state, action.astype(np.int32), 7)
+        np.testing.assert_array_equal(to_np(nxt), e_next)
+        np.testing.assert_array_equal(to_np(done), e_done)
