@@ -136,3 +136,28 @@ def test_trig_by_dtype_dispatch():
     assert np.array_equal(sin_f(x32), dm.sin(x32)) and sin_f(x32).dtype == np.float32
     x64 = x32.astype(np.float64)
     assert np.array_equal(cos_f(x64), dm.sincos64(x64)[1]) and cos_f(x64).dtype == np.float64
+
+
+def test_reduction_is_the_identity_within_078():
+    """The kernels' near-rest vote (one wave vote, then the polynomial alone) relies on the
+    reduction returning the argument itself (bit for bit but for -0, which reduces to +0;
+    both give the same sin and cos) with quadrant 0, for |x| <= 0.78. Checked for every
+    float32 in [0.5, 0.78] of both signs (below 0.5, x * 2/pi < 0.32 and rint gives 0), for
+    random smaller magnitudes, and for the zeros and subnormals; and the first
+    float32 above 0.78 still has quadrant 0 (the bound is conservative)."""
+    lo, hi = np.float32(0.5).view(np.uint32), np.float32(0.78).view(np.uint32)
+    pos = np.arange(lo, hi + 1, dtype=np.uint32).view(np.float32)
+    small = np.random.default_rng(78).uniform(0, 0.5, 1_000_000).astype(np.float32)
+    special = np.array([0.0, 1e-45, 1e-40, 1.17549435e-38, 1e-30], dtype=np.float32)
+    x = np.concatenate([pos, -pos, small, -small, special, -special])
+    for part in np.array_split(x, 8):
+        r, q = dm._reduce(part)
+        same = r.view(np.uint32) == part.view(np.uint32)
+        assert np.all(same | ((part == 0) & (r == 0)))
+        assert not q.any()
+        s, c = dm.sincos(part)
+        ps, pc = dm._poly(part)
+        assert np.array_equal(s.view(np.uint32), ps.view(np.uint32))
+        assert np.array_equal(c.view(np.uint32), pc.view(np.uint32))
+    above = np.nextafter(np.float32(0.78), np.float32(1.0))
+    assert dm._reduce(np.array([above]))[1][0] == 0
