@@ -731,24 +731,32 @@ __device__ __forceinline__ void policy_group(const float* __restrict__ w, const 
 #pragma unroll
   for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
   constexpr int kUnits = (HID + G - 1) / G;
-  // every weight of the lane's hidden units is loaded before the first use (one memory round
-  // trip); left to itself the scheduler may wait out one round trip per weight
-  float wu[kUnits][1 + OBS];
-#pragma unroll
-  for (int u = 0; u < kUnits; ++u) {
-    const int j = g + G * u < HID ? g + G * u : 0;  // lanes past HID recompute unit 0, unused
-    wu[u][0] = w[R::b1(j) * kStride];
-#pragma unroll
-    for (int k = 0; k < OBS; ++k) wu[u][1 + k] = w[R::w1(k, j) * kStride];
-  }
-  __builtin_amdgcn_sched_barrier(0);
+  // the weights of the lane's hidden units are loaded in two batches (one for fewer than
+  // eight units), each before its first use: two memory round trips. Left to itself the
+  // scheduler may wait out one round trip per weight; one batch of all sixteen units at
+  // H = 64 holds 160-224 weights at once and made the biped's kernel spill.
+  constexpr int kBatch = kUnits >= 8 ? kUnits / 2 : kUnits;
+  static_assert(kUnits % kBatch == 0, "whole batches");
   float hs[kUnits];
 #pragma unroll
-  for (int u = 0; u < kUnits; ++u) {
-    float sj = wu[u][0];
+  for (int u0 = 0; u0 < kUnits; u0 += kBatch) {
+    float wu[kBatch][1 + OBS];
 #pragma unroll
-    for (int k = 0; k < OBS; ++k) sj = sj + obs[k] * wu[u][1 + k];
-    hs[u] = det_tanh(sj);
+    for (int b = 0; b < kBatch; ++b) {
+      const int j = g + G * (u0 + b) < HID ? g + G * (u0 + b) : 0;  // lanes past HID recompute unit 0, unused
+      wu[b][0] = w[R::b1(j) * kStride];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) wu[b][1 + k] = w[R::w1(k, j) * kStride];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      float sj = wu[b][0];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) sj = sj + obs[k] * wu[b][1 + k];
+      hs[u0 + b] = det_tanh(sj);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
   __syncthreads();  // the rows' previous readers are done
 #pragma unroll
