@@ -679,7 +679,8 @@ __device__ __forceinline__ void policy_torques(const float* __restrict__ w, int6
   // trip whatever the scheduler would otherwise interleave (left to itself it has waited on
   // the biped's weights one at a time). Two units at C = 4 keep two waves per SIMD (236
   // registers; four-unit batches took 318); four at C <= 2 (169 registers) match the
-  // biped's rollout before this form (ES rollout 25.0 ms at 8 sweeps; two units: 25.5).
+  // biped's rollout before this form (ES rollout 25.0 ms at 8 sweeps; two units: 25.5;
+  // eight units, 227 registers, were no faster).
   constexpr int kWant = C <= 2 ? 4 : 2;
   constexpr int kBatch = kWant <= HID ? kWant : HID;
   static_assert(HID % kBatch == 0, "whole batches of hidden units");
