@@ -653,6 +653,308 @@ __global__ __launch_bounds__(kBlock) void step_euler_staged_kernel(const float* 
   stream_store((uint8_t)(d ? 1 : 0), done + e);
 }
 
+// ---------------------------------------------------------------------------
+// Staged RK4 step for long chains (K = 32, 64): the reference's drop-in step
+// (pendulum_aba_np.py:117-123, pendulum_aba_metal.py:85-116) with the per-link state kept
+// by lifetime, as in the staged Euler kernel. The generic RK4 kernel holds nine per-link
+// arrays per evaluation next to the stage sums, and past K = 16 keeps them in scratch
+// memory. Here, per evaluation:
+// - pass 1 (outward) forms the joint angles and rates from the stage input (t, o), writes
+//   the joints' sin and cos into the LDS rows and keeps each link's velocity (3 floats);
+// - pass 2 (inward) trades each link's velocity for U and u (4 floats), reading the
+//   joint rate back from o;
+// - pass 3 (outward) repeats the velocity recursion next to the accelerations (the same
+//   operations on the same values, so the same bits), and finishes each link's stage at
+//   once: the stage sums and the next stage's input (t, o), or in the last stage the
+//   link's update, wrap and clip, stored.
+// Across the stages each lane keeps t, o and (kSumsInNext false) the stage sums of the
+// angles and velocities in registers; with kSumsInNext the sums live in the output rows of
+// `next` between stages (the lane's own column, overwritten by the result in the last
+// stage), which is what fits 64 links in the register file. Every value is the generic
+// kernel's, from the same operations in the same order (rk4, terminal, store_with_reset).
+// ---------------------------------------------------------------------------
+
+// Pass 1 of one evaluation: joint angles and rates from (t, o), the joints' sin and cos
+// into the LDS rows (the polynomial alone when the caller's wave vote found every joint
+// angle within 0.78 of zero), link velocities in link frames (pendulum_aba_np.py:36-50).
+template <int K, bool kNear>
+__device__ __forceinline__ void rk4_outward(const float (&t)[K], const float (&o)[K], float* sn_l, float* cs_l,
+                                            float (&vw)[K], float (&vx)[K], float (&vy)[K]) {
+  float w = 0.0f, x = 0.0f, y = 0.0f;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const float q = (i == 0) ? t[0] : t[i] - t[i > 0 ? i - 1 : 0];
+    const float qd = (i == 0) ? o[0] : o[i] - o[i > 0 ? i - 1 : 0];
+    float sn, cs;
+    if constexpr (kNear)
+      sincos_poly(q, &sn, &cs);
+    else
+      det_sincos(q, &sn, &cs);
+    sn_l[i * kBlock] = sn;
+    cs_l[i * kBlock] = cs;
+    const float xy = (i == 0) ? (y + w * 0.0f) : (y + w);
+    const float nw = w + qd;
+    const float nx = cs * x + sn * xy;
+    const float ny = (-sn) * x + cs * xy;
+    vw[i] = nw;
+    vx[i] = nx;
+    vy[i] = ny;
+    w = nw;
+    x = nx;
+    y = ny;
+  }
+}
+
+// Pass 2 of one evaluation (pendulum_aba_np.py:51-82): staged_inward with the joint rates
+// read back from o instead of kept per link.
+template <int K, class Div>
+__device__ __forceinline__ void rk4_inward(const float (&vw)[K], const float (&vx)[K], const float (&vy)[K],
+                                           const float (&o)[K], const float* cs_l, const float* sn_l, float tq,
+                                           float (&U0)[K], float (&U1)[K], float (&U2)[K], float (&uu)[K],
+                                           float (&cv)[K], float (&sv)[K], Div& div) {
+  float A0 = 1.0f, A1 = 0.0f, A2 = 1.0f, A3 = 1.0f, A4 = 0.0f, A5 = 1.0f;
+  float P0, P1, P2;
+  own_bias(vw[K - 1], vx[K - 1], vy[K - 1], P0, P1, P2);
+#pragma unroll
+  for (int j = K - 1; j >= 1 && j > K - 1 - kStageLinks; --j) {
+    cv[j] = cs_l[j * kBlock];
+    sv[j] = sn_l[j * kBlock];
+  }
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) {
+    U0[i] = A0;
+    U1[i] = A1;
+    U2[i] = A2;
+    uu[i] = (i == 0 ? tq : 0.0f) - P0;
+    if (i == 0) break;
+    if (i - kStageLinks >= 1) {
+      cv[i - kStageLinks] = cs_l[(i - kStageLinks) * kBlock];
+      sv[i - kStageLinks] = sn_l[(i - kStageLinks) * kBlock];
+    }
+    const float D = A0;
+    const double rD = recip(D);
+    const float I0 = A0 - div(A0 * A0, D, rD), I1 = A1 - div(A0 * A1, D, rD), I2 = A2 - div(A0 * A2, D, rD);
+    const float I3 = A3 - div(A1 * A1, D, rD), I4 = A4 - div(A1 * A2, D, rD), I5 = A5 - div(A2 * A2, D, rD);
+    const float qd = o[i] - o[i - 1];
+    const float c1 = qd * vy[i], c2 = (-qd) * vx[i];
+    const float Iac0 = I1 * c1 + I2 * c2;
+    const float Iac1 = I3 * c1 + I4 * c2;
+    const float Iac2 = I4 * c1 + I5 * c2;
+    const float g = div(uu[i], D, rD);
+    const float pa0 = (P0 + Iac0) + A0 * g;
+    const float pa1 = (P1 + Iac1) + A1 * g;
+    const float pa2 = (P2 + Iac2) + A2 * g;
+    const float c = cv[i], s = sv[i];
+    const float B00 = (I0 + I1 * s) + I2 * c, B01 = I1 * c - I2 * s, B02 = I1 * s + I2 * c;
+    const float B10 = (I1 + I3 * s) + I4 * c, B11 = I3 * c - I4 * s, B12 = I3 * s + I4 * c;
+    const float B20 = (I2 + I4 * s) + I5 * c, B21 = I4 * c - I5 * s, B22 = I4 * s + I5 * c;
+    A0 = 1.0f + ((B00 + s * B10) + c * B20);
+    A1 = (B01 + s * B11) + c * B21;
+    A2 = 1.0f + ((B02 + s * B12) + c * B22);
+    A3 = 1.0f + (c * B11 - s * B21);
+    A4 = c * B12 - s * B22;
+    A5 = 1.0f + (s * B12 + c * B22);
+    float pp0, pp1, pp2;
+    own_bias(vw[i - 1], vx[i - 1], vy[i - 1], pp0, pp1, pp2);
+    P0 = ((pp0 + pa0) + s * pa1) + c * pa2;
+    P1 = (pp1 + c * pa1) - s * pa2;
+    P2 = (pp2 + s * pa1) + c * pa2;
+    if ((i & (kStageLinks - 1)) == 0) asm volatile("" ::: "memory");  // LDS reads kStageLinks links ahead at most
+  }
+}
+
+// Passes 1 and 2 of one evaluation; the quotients of pass 2 through the pivots' shared
+// float64 reciprocals when kRecip (a lane on which one came out subnormal runs both passes
+// again with IEEE division, from t and o, which no pass writes), else IEEE division.
+// o's values passed through an empty asm statement: the same bits, but values the compiler
+// cannot match with the earlier ones, so a pass that recomputes a joint rate o[i] - o[i-1]
+// does not keep the previous pass's copy alive across the passes in between (K more
+// registers live).
+template <int K>
+__device__ __forceinline__ void opaque_rows(float (&o)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) asm volatile("" : "+v"(o[i]));
+}
+
+template <int K, bool kRecip>
+__device__ __forceinline__ void rk4_passes12(const float (&t)[K], float (&o)[K], float* sn_l, float* cs_l,
+                                             float tq, float (&U0)[K], float (&U1)[K], float (&U2)[K],
+                                             float (&uu)[K], float (&cv)[K], float (&sv)[K]) {
+  // one wave vote for the K joint angles of this stage
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < K; ++i) ok &= fabsf((i == 0) ? t[0] : t[i] - t[i > 0 ? i - 1 : 0]) <= 0.78f;
+  const bool near = __all(ok);
+  float vw[K], vx[K], vy[K];
+  if (near)
+    rk4_outward<K, true>(t, o, sn_l, cs_l, vw, vx, vy);
+  else
+    rk4_outward<K, false>(t, o, sn_l, cs_l, vw, vx, vy);
+  asm volatile("" ::: "memory");  // each pass reads its LDS rows in its own order
+  opaque_rows<K>(o);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kRecip) {
+    DivRecip fast;
+    rk4_inward<K>(vw, vx, vy, o, cs_l, sn_l, tq, U0, U1, U2, uu, cv, sv, fast);
+    if (fast.saw_subnormal()) {
+      asm volatile("" ::: "memory");
+      if (near)
+        rk4_outward<K, true>(t, o, sn_l, cs_l, vw, vx, vy);
+      else
+        rk4_outward<K, false>(t, o, sn_l, cs_l, vw, vx, vy);
+      asm volatile("" ::: "memory");
+      DivIEEE ieee;
+      rk4_inward<K>(vw, vx, vy, o, cs_l, sn_l, tq, U0, U1, U2, uu, cv, sv, ieee);
+    }
+  } else {
+    DivIEEE ieee;
+    rk4_inward<K>(vw, vx, vy, o, cs_l, sn_l, tq, U0, U1, U2, uu, cv, sv, ieee);
+  }
+  asm volatile("" ::: "memory");
+}
+
+// Pass 3 of evaluation kStage (0..3): accelerations from a base accelerating at -g
+// (pendulum_aba_np.py:83-99) with the velocity recursion repeated, and each link's stage
+// finished (rk4's stage loops, in the same order). The input rows th, om are re-read
+// kStageLinks links ahead (stage 0 has them in t, o); with kSumsInNext the stage sums are
+// read from and written to the lane's column of `next`.
+template <int K, int kStage, bool kSumsInNext>
+__device__ __forceinline__ void rk4_pass3(const RowBuffer& in, const RowBuffer& out, const float* cs_l,
+                                          const float* sn_l, const float (&U0)[K], const float (&U1)[K],
+                                          const float (&U2)[K], const float (&uu)[K], float (&cv)[K], float (&sv)[K],
+                                          float (&t)[K], float (&o)[K], float (&sth)[K], float (&som)[K]) {
+  constexpr bool kReread = kStage > 0;               // stage 0's t, o are the inputs themselves
+  constexpr bool kReadSums = kSumsInNext && kStage > 0;
+  float thv[K], omv[K], stv[K], sov[K];              // rotating read-ahead registers
+#pragma unroll
+  for (int j = 0; j < K && j < kStageLinks; ++j) {
+    cv[j] = cs_l[j * kBlock];
+    sv[j] = sn_l[j * kBlock];
+    if constexpr (kReread) {
+      thv[j] = in.load(j);
+      omv[j] = in.load(K + j);
+    }
+    if constexpr (kReadSums) {
+      stv[j] = out.load(j);
+      sov[j] = out.load(K + j);
+    }
+  }
+  float aw = 0.0f, ax = -GRAVITY, ay = 0.0f, run = 0.0f;
+  float w = 0.0f, x = 0.0f, y = 0.0f, o_prev = 0.0f;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if (i + kStageLinks < K) {
+      cv[i + kStageLinks] = cs_l[(i + kStageLinks) * kBlock];
+      sv[i + kStageLinks] = sn_l[(i + kStageLinks) * kBlock];
+      if constexpr (kReread) {
+        thv[i + kStageLinks] = in.load(i + kStageLinks);
+        omv[i + kStageLinks] = in.load(K + i + kStageLinks);
+      }
+      if constexpr (kReadSums) {
+        stv[i + kStageLinks] = out.load(i + kStageLinks);
+        sov[i + kStageLinks] = out.load(K + i + kStageLinks);
+      }
+    }
+    const float o_i = o[i];
+    const float qd = (i == 0) ? o_i : o_i - o_prev;
+    const float c = cv[i], s = sv[i];
+    const float vxy = (i == 0) ? (y + w * 0.0f) : (y + w);
+    const float nw = w + qd;
+    const float nx = c * x + s * vxy;
+    const float ny = (-s) * x + c * vxy;
+    w = nw;
+    x = nx;
+    y = ny;
+    const float c1 = qd * ny, c2 = (-qd) * nx;
+    const float xy = (i == 0) ? (ay + aw * 0.0f) : (ay + aw);
+    const float ap0 = aw;
+    const float ap1 = (c * ax + s * xy) + c1;
+    const float ap2 = ((-s) * ax + c * xy) + c2;
+    const float qdd = (uu[i] - ((U0[i] * ap0 + U1[i] * ap1) + U2[i] * ap2)) / U0[i];
+    aw = ap0 + qdd;
+    ax = ap1;
+    ay = ap2;
+    run = run + qdd;
+    const float acc = run;
+    const float th_i = kReread ? thv[i] : t[i];
+    const float om_i = kReread ? omv[i] : o_i;
+    float st, so;  // the stage sums before this stage
+    if constexpr (kStage > 0) {
+      st = kSumsInNext ? stv[i] : sth[i];
+      so = kSumsInNext ? sov[i] : som[i];
+    }
+    if constexpr (kStage < 3) {
+      if constexpr (kStage == 0) {
+        st = o_i;
+        so = acc;
+      } else {
+        st = st + 2.0f * o_i;
+        so = so + 2.0f * acc;
+      }
+      if constexpr (kSumsInNext) {
+        out.store(i, st);
+        out.store(K + i, so);
+      } else {
+        sth[i] = st;
+        som[i] = so;
+      }
+      constexpr float h = kStage == 2 ? DT : DT_2;
+      t[i] = th_i + h * o_i;
+      o[i] = om_i + h * acc;
+    } else {
+      const float th_new = wrap(th_i + DT_6 * (st + o_i));
+      out.store(i, th_new);
+      out.store(K + i, clip(om_i + DT_6 * (so + acc), -MAX_VEL, MAX_VEL));
+      t[i] = th_new;  // kept for the termination test
+    }
+    o_prev = o_i;
+    if ((i & (kStageLinks - 1)) == kStageLinks - 1) asm volatile("" ::: "memory");
+  }
+}
+
+template <int K, int kStage, bool kSumsInNext, bool kRecip>
+__device__ __forceinline__ void rk4_stage(const RowBuffer& in, const RowBuffer& out, float* sn_l, float* cs_l, float tq,
+                                          float (&t)[K], float (&o)[K], float (&sth)[K], float (&som)[K]) {
+  float U0[K], U1[K], U2[K], uu[K], cv[K], sv[K];
+  rk4_passes12<K, kRecip>(t, o, sn_l, cs_l, tq, U0, U1, U2, uu, cv, sv);
+  opaque_rows<K>(o);
+  __builtin_amdgcn_sched_barrier(0);
+  rk4_pass3<K, kStage, kSumsInNext>(in, out, cs_l, sn_l, U0, U1, U2, uu, cv, sv, t, o, sth, som);
+  asm volatile("" ::: "memory");
+}
+
+template <int K, bool kSumsInNext, bool kRecip>
+__global__ __launch_bounds__(kBlock) void step_rk4_staged_kernel(const float* __restrict__ state,
+                                                                 const int32_t* __restrict__ action, uint32_t seed,
+                                                                 float* __restrict__ next, float* __restrict__ reward,
+                                                                 uint8_t* __restrict__ done, int64_t n) {
+  __shared__ float trig_lds[2 * K * kBlock];
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n) return;
+  float* sn_l = trig_lds + threadIdx.x;  // sin of joint i at sn_l[i * kBlock]
+  float* cs_l = trig_lds + K * kBlock + threadIdx.x;
+  const float tq = (float)(stream_load(action + e) - 1) * 1.0f;
+  const RowBuffer in(state, 2 * K, n, e), out(next, 2 * K, n, e);
+  float t[K], o[K], sth[K], som[K];  // sth, som unused (no registers) with kSumsInNext
+#pragma unroll
+  for (int p = 0; p < K; ++p) {
+    t[p] = in.load(p);
+    o[p] = in.load(K + p);
+  }
+  rk4_stage<K, 0, kSumsInNext, kRecip>(in, out, sn_l, cs_l, tq, t, o, sth, som);
+  rk4_stage<K, 1, kSumsInNext, kRecip>(in, out, sn_l, cs_l, tq, t, o, sth, som);
+  rk4_stage<K, 2, kSumsInNext, kRecip>(in, out, sn_l, cs_l, tq, t, o, sth, som);
+  rk4_stage<K, 3, kSumsInNext, kRecip>(in, out, sn_l, cs_l, tq, t, o, sth, som);
+  const bool d = terminal<K, K>(t);
+  if (d) {  // every row U[+-0.1], overwriting the stepped state
+    const uint32_t h = env_hash(seed, (uint32_t)e);
+#pragma unroll
+    for (int p = 0; p < 2 * K; ++p) out.store(p, uniform_pm(pcg_hash(h + (uint32_t)p * kRowStride), RESET_BOUND));
+  }
+  stream_store(d ? 0.0f : -1.0f, reward + e);
+  stream_store((uint8_t)(d ? 1 : 0), done + e);
+}
+
 template <int K>
 __global__ __launch_bounds__(kBlock) void accelerations_kernel(const float* __restrict__ state,
                                                                const float* __restrict__ torque,
@@ -693,6 +995,20 @@ __global__ __launch_bounds__(kBlock) void reset_kernel(float* __restrict__ state
 #endif
 constexpr int kStagedEulerMinK = ABA_STAGED_EULER_MIN_K;
 
+// Chains at least this long take the staged RK4 kernel; up to ABA_RK4_SUMS_IN_REGS_MAX_K links
+// it keeps the stage sums in registers (past it, in the output rows), and up to
+// ABA_RK4_RECIP_MAX_K links it divides through the pivots' shared reciprocals.
+#ifndef ABA_STAGED_RK4_MIN_K
+#define ABA_STAGED_RK4_MIN_K 32
+#endif
+#ifndef ABA_RK4_SUMS_IN_REGS_MAX_K
+#define ABA_RK4_SUMS_IN_REGS_MAX_K 32
+#endif
+#ifndef ABA_RK4_RECIP_MAX_K
+#define ABA_RK4_RECIP_MAX_K 32
+#endif
+constexpr int kStagedRk4MinK = ABA_STAGED_RK4_MIN_K;
+
 enum Op { kRk4, kEulerArray, kEulerRng, kAcc, kReset, kResetZeroVel, kMassRk4, kMassAcc };
 
 template <int K>
@@ -700,9 +1016,21 @@ int launch(Op op, const float* state, const void* in, uint32_t seed, float* out,
            int64_t n, hipStream_t s) {
   const dim3 grid(grid_for(n)), block(kBlock);
   switch (op) {
-    case kRk4:
-      hipLaunchKernelGGL(step_rk4_kernel<K>, grid, block, 0, s, state, (const int32_t*)in, seed, out, reward, done, n);
+    case kRk4: {
+      // the staged kernel addresses the (2K, n) arrays with 32-bit byte offsets
+      const bool staged = K >= kStagedRk4MinK && (int64_t)2 * K * n * 4 < ((int64_t)1 << 31);
+      if constexpr (K >= kStagedRk4MinK) {
+        constexpr bool kSumsInNext = K > ABA_RK4_SUMS_IN_REGS_MAX_K;
+        constexpr bool kRecip = K <= ABA_RK4_RECIP_MAX_K;
+        if (staged)
+          hipLaunchKernelGGL((step_rk4_staged_kernel<K, kSumsInNext, kRecip>), grid, block, 0, s, state,
+                             (const int32_t*)in, seed, out, reward, done, n);
+      }
+      if (!staged)
+        hipLaunchKernelGGL(step_rk4_kernel<K>, grid, block, 0, s, state, (const int32_t*)in, seed, out, reward, done,
+                           n);
       break;
+    }
     case kEulerArray:
     case kEulerRng: {
       // the staged kernel addresses the (2K, n) arrays with 32-bit byte offsets

@@ -118,6 +118,50 @@ def test_k64_euler_full_size_with_terminations(dev):
     np.testing.assert_array_equal(to_np(ns), ens)
 
 
+@pytest.mark.parametrize("k", [32, 64])
+def test_rk4_full_size_with_terminations(dev, k):
+    """The staged RK4 kernel (K = 32, 64) at the benchmark's N = 65,536: one step bit for bit
+    against the oracle, with chains pointing up (terminated, every row reset U[+-0.1]) in
+    some columns, random wide chains in most and near-rest chains in the first 4,096 (64
+    waves that take the sin/cos polynomial)."""
+    from hipenvs import pendulum_aba
+
+    n = 65_536
+    state, action = random_state(k, n, seed=640 + k)
+    state[:, :4096] = oaba.Pendulum(k).reset(4096, seed=12)
+    state[:k, 4096::89] = np.float32(np.pi)
+    p = pendulum_aba.Pendulum(k)
+    p.reseed(12)
+    ns, rew, done = p.step(torch.from_numpy(state).to(dev), torch.from_numpy(action.astype(np.int32)).to(dev))
+    ens, erew, edone = oaba.Pendulum(k).step(state, action, seed=13)
+    assert edone.sum() >= (n - 4096) // 89
+    np.testing.assert_array_equal(to_np(done), edone)
+    np.testing.assert_array_equal(to_np(rew), erew)
+    np.testing.assert_array_equal(to_np(ns), ens)
+
+
+@pytest.mark.parametrize("k", [4, 16, 32, 64])
+def test_rk4_reference_benchmark_chain(dev, k):
+    """The reference's own benchmark shape for the RK4 drop-in (bench_aba.py:26-37): every
+    row from the reset distribution, uniform actions in {0, 1, 2}, free-running; 16 steps at
+    2,048 envs with identical states and flags."""
+    from hipenvs import pendulum_aba
+
+    n = 2048
+    p = pendulum_aba.Pendulum(k)
+    ref = oaba.Pendulum(k)
+    s_dev = p.reset(n, seed=0, device=dev)
+    s_ref = ref.reset(n, seed=0)
+    np.testing.assert_array_equal(to_np(s_dev), s_ref)
+    p.reseed(0)
+    for t in range(1, 17):
+        act = rng.uniform_actions(500 + t, n, 3)
+        s_dev, _, d_dev = p.step(s_dev, torch.from_numpy(act).to(dev))
+        s_ref, _, d_ref = ref.step(s_ref, act, seed=t)
+        np.testing.assert_array_equal(to_np(d_dev), d_ref, err_msg=f"step {t}")
+    np.testing.assert_array_equal(to_np(s_dev), s_ref)
+
+
 def near_rest_states(k, seed):
     """Angles U[-0.38, 0.38] (every joint angle and every angle within 0.78 of zero), zero
     velocities, in six waves of 64 envs: waves 0 and 1 stay within the bound (wave 1 with one
