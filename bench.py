@@ -100,6 +100,10 @@ CARTPOLE_BYTES = 41
 # profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
 ABA_TRAFFIC = {4: 4649746, 16: 17437438, 64: 99818014}
+ABA_RK4_TRAFFIC = {}
+# The reference's articulated-body kernel (RK4, eval every 32) at N = 65,536 on its M3 Pro,
+# results/aba.csv:137,222,307,392,460 (K = 4, 8, 16, 32, 64).
+ABA_RK4_REFERENCE = {4: 450437382, 8: 184284347, 16: 68215640, 32: 17807725, 64: 3961767}
 STEP_BODY_TRAFFIC = {"pendulum_k2": 2833253, "pendulum_k4": 5104345, "pendulum_k8": 9586116,
                      "pendulum_k16": 19185779, "hopper": 4889324, "acrobot": 10906005, "legged4_s8": 8227360,
                      "legged4_s8_reference": 16402468}
@@ -342,6 +346,20 @@ def module_api_rate(n, steps, dev):
 # profiles/cartpole_step_n262144.md tabulates them. The tracer runs each dispatch on its own,
 # so these include the per-dispatch ramp and drain that back-to-back launches overlap.
 CARTPOLE_TRACE_NS = {1 << 18: 3561.5, 1 << 20: 8518.8, 1 << 24: 110860.0}
+# sha256 (first 16 hex digits) of the sources the traced kernel was built from,
+# csrc/cartpole.hip then csrc/hipenvs_device.h: when the sources differ, the trace no longer
+# describes this build, and cartpole_roofline falls back to the run's own HIP-event figure.
+CARTPOLE_TRACE_SOURCE_SHA = "056ec841d737ef48"
+CARTPOLE_TRACE_SOURCES = ("metal-rl-envs_amd/csrc/cartpole.hip", "metal-rl-envs_amd/csrc/hipenvs_device.h")
+
+
+def cartpole_source_sha():
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in CARTPOLE_TRACE_SOURCES:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
 
 
 def cartpole_roofline(n, kernel_only):
@@ -349,10 +367,13 @@ def cartpole_roofline(n, kernel_only):
     secondary from this run's back-to-back HIP-event launch time."""
     bytes_launch = CARTPOLE_BYTES * n
     events_gbs = kernel_only["achieved_gbs_events"]
-    trace_ns = CARTPOLE_TRACE_NS.get(n)
+    current = cartpole_source_sha() == CARTPOLE_TRACE_SOURCE_SHA
+    trace_ns = CARTPOLE_TRACE_NS.get(n) if current else None
     achieved = bytes_launch / (trace_ns * 1e-9) / 1e9 if trace_ns else events_gbs
     return {"bound": "hbm", "kernel": "cp::step_kernel", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(n),
+            "frac": achieved / HBM_PEAK_GBS, "traffic": CARTPOLE_TRAFFIC.get(n) if current else None,
+            "frac_source": "kernel trace" if trace_ns else "hip events (this run)",
+            "trace_matches_sources": current,
             "algorithmic_bytes_per_launch": bytes_launch, "avg_launch_ns_trace": trace_ns,
             "avg_launch_ns_events": kernel_only["us_per_launch_events"] * 1e3,
             "achieved_events": events_gbs, "frac_events": events_gbs / HBM_PEAK_GBS}
@@ -860,6 +881,68 @@ def bench_aba(dev, steps=1000, n=65536, ks=(4, 16, 64)):
     return out
 
 
+def bench_aba_rk4(dev, steps=64, n=65536, ks=(4, 16, 32, 64), region_seconds=0.1):
+    """The reference's own ABA benchmark (bench_aba.py:26-37 through bench.py:48-61): the RK4
+    drop-in step (dt 0.02, torque (a - 1) for a in {0, 1, 2}) at N = 65,536 from the reset
+    distribution (all 2K rows U[+-0.1]), every iteration drawing its actions on the device and
+    stepping, every reward and done kept; `steps` iterations per HIP graph, replayed back to back.
+    Also the step alone on actions drawn before the clock (HIP events on the replay stream),
+    with its HBM roofline at 16K + 9 algorithmic bytes per env-step."""
+    import torch
+
+    from hipenvs import _lib, cartpole, pendulum_aba
+
+    P = _lib.ptr
+    fn = _lib.lib().hipenvs_pendulum_aba_step
+    sampler = _lib.lib().hipenvs_sample_actions
+    out = {}
+    for k in ks:
+        body_ = pendulum_aba.Pendulum(k)
+        bufs = [body_.reset(n, seed=0, device=dev), torch.empty((2 * k, n), device=dev)]
+        rewards = torch.empty((steps, n), device=dev)
+        dones = torch.empty((steps, n), dtype=torch.bool, device=dev)
+        row = torch.empty(n, dtype=torch.int32, device=dev)
+        actions = torch.empty((steps, n), dtype=torch.int32, device=dev)
+        for t in range(steps):
+            cartpole.sample_actions(n, m=3, seed=1 + t, device=dev, out=actions[t])
+
+        def sampled(s):
+            for t in range(steps):
+                rc = sampler(P(row), n, 3, 1 + t, s)
+                if rc != 0:
+                    raise RuntimeError(f"hipenvs_sample_actions failed: {rc}")
+                rc = fn(k, P(bufs[t % 2]), P(row), t + 1, P(bufs[(t + 1) % 2]), P(rewards[t]), P(dones[t]), n, s)
+                if rc != 0:
+                    raise RuntimeError(f"aba rk4 step failed: {rc}")
+
+        def alone(s):
+            for t in range(steps):
+                rc = fn(k, P(bufs[t % 2]), P(actions[t]), t + 1, P(bufs[(t + 1) % 2]), P(rewards[t]), P(dones[t]), n,
+                        s)
+                if rc != 0:
+                    raise RuntimeError(f"aba rk4 step failed: {rc}")
+
+        g = capture_graph(dev, sampled)
+        per_region = replays_for(g, region_seconds)
+        wall, _ = time_replay(g, 3, per_region)
+        its = steps * per_region
+        ga = capture_graph(dev, alone)
+        _, ev = time_replay(ga, 3, per_region)
+        launch = ev / its
+        bytes_step = 16 * k + 9  # 2K floats in and out, action, reward, done
+        achieved = bytes_step * n / launch / 1e9
+        out[str(k)] = {"n_envs": n, "steps_per_graph": steps, "replays_per_region": per_region,
+                       "env_steps_per_s": n * its / wall, "us_per_iteration": wall / its * 1e6,
+                       "step_alone_us_per_launch": launch * 1e6, "bytes_per_env_step": bytes_step,
+                       "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                    "frac": achieved / HBM_PEAK_GBS, "traffic": ABA_RK4_TRAFFIC.get(k)},
+                       "reference_m3pro_env_steps_per_s": ABA_RK4_REFERENCE.get(k)}
+        log(f"ABA RK4 K={k} N={n}: {n * its / wall:,.0f} env-steps/s (sampler + step), step alone "
+            f"{launch * 1e6:.2f} us per launch, {achieved:.0f} GB/s algorithmic")
+        del g, ga, bufs, rewards, dones, actions
+    return out
+
+
 def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
     """The reference's remaining step modules: the mass-matrix K-link pendulum (RK4, actions
     drawn per step on the device) and the hopper, graph-replayed like the ABA step."""
@@ -978,6 +1061,7 @@ def main():
             extra[f"legged{c}_es_rollout"] = legged
     if args.only in ("aba", "steps"):
         extra["aba_euler"] = bench_aba(dev)
+        extra["aba_rk4"] = bench_aba_rk4(dev)
         if args.only == "steps":
             extra["step_bodies"] = bench_step_bodies(dev)
         print(json.dumps(extra), flush=True)
@@ -1005,6 +1089,7 @@ def main():
                                                  f"{its} steps"}
                 rec["speedup_vs_cpu"] = rec["env_steps_per_s"] / rate
                 log(f"ABA K={k} numpy: {rate:,.0f} env-steps/s -> GPU {rec['speedup_vs_cpu']:,.0f}x")
+        extra["aba_rk4"] = bench_aba_rk4(dev)
         extra["step_bodies"] = bench_step_bodies(dev)
 
     cpu = None
