@@ -420,3 +420,54 @@ def train(cfg, backend_name, seed, log=None, device=None):
             log(rec.generation, rec.env_steps, rec.train_seconds, rec.pop_fitness, rec.score)
         if trainer.solved or trainer.exhausted:
             return Result(trainer.solved, rec.generation, rec.env_steps, rec.train_seconds, rec.score)
+
+
+# The reference's backend names on the command line: its fused Metal rollout is the
+# "fused" backend here and its MLX step loop the "loop" backend; its numpy backend is the
+# CPU oracle, which this package does not run.
+BACKEND_ALIASES = {"metal": "fused", "mlx": "loop"}
+
+
+def parse_args(argv=None):
+    """(Config, backend name, seed) from the reference's command line (``es.py:357-371``):
+    the same flags with the same defaults, plus ``--hidden`` and ``--horizon`` and the
+    "seeded" backend, which the reference does not have."""
+    import argparse
+
+    p = argparse.ArgumentParser(prog="python -m hipenvs.es", description=__doc__,
+                                formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--task", choices=sorted(TASKS), default="cartpole")
+    p.add_argument("--pop", type=int, default=1024)
+    p.add_argument("--backend", choices=sorted(BACKENDS) + sorted(BACKEND_ALIASES), default="metal")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--lr", type=float, default=0.1)
+    p.add_argument("--sigma", type=float, default=0.1)
+    p.add_argument("--time-budget", type=float, default=120.0)
+    p.add_argument("--max-generations", type=int, default=500)
+    p.add_argument("--assist", type=float, default=0.0,
+                   help="torso-assist spring stiffness at generation 1, annealed to zero")
+    p.add_argument("--start-velocity", type=float, default=0.0,
+                   help="forward push at episode start, annealed to zero")
+    p.add_argument("--anneal", type=int, default=300, help="generation by which both curricula reach zero")
+    p.add_argument("--hidden", type=int, default=None, help="hidden units (default: the task's)")
+    p.add_argument("--horizon", type=int, default=500)
+    a = p.parse_args(argv)
+    cfg = Config(task=a.task, pop=a.pop, hidden=a.hidden, sigma=a.sigma, lr=a.lr, horizon=a.horizon,
+                 max_generations=a.max_generations, time_budget=a.time_budget, assist_k0=a.assist,
+                 start_velocity=a.start_velocity, anneal_gens=a.anneal)
+    return cfg, BACKEND_ALIASES.get(a.backend, a.backend), a.seed
+
+
+def main(argv=None):
+    """The reference's ``python es.py ...`` (``es.py:357-382``): train and print each
+    generation, then the result."""
+    cfg, backend, seed = parse_args(argv)
+    result = train(cfg, backend, seed, log=lambda gen, es_, secs, fit, score: print(
+        f"gen {gen:4d}  env_steps {es_:>13,}  train {secs:7.2f}s  pop fitness {fit:8.1f}  score {score:8.1f}",
+        flush=True))
+    print(result)
+    return result
+
+
+if __name__ == "__main__":
+    main()

@@ -63,3 +63,24 @@ def test_curriculum_anneals():
     cfg = es.Config(task="cartpole", assist_k0=20.0, start_velocity=0.3, anneal_gens=100)
     assert es.curriculum(cfg, 1) == (20.0, 0.3) and es.curriculum(cfg, 51) == (10.0, 0.15)
     assert es.curriculum(cfg, 101) == (0.0, 0.0)
+
+
+def test_command_line_matches_the_reference_defaults():
+    """es.py:357-371: the same flags and defaults (task cartpole, pop 1,024, backend metal,
+    seed 0, lr 0.1, sigma 0.1, 120 s, 500 generations, no curricula, anneal 300); the
+    reference's backend names map onto this package's backends."""
+    cfg, backend, seed = es.parse_args([])
+    assert (cfg.task, cfg.pop, backend, seed, cfg.lr, cfg.sigma) == ("cartpole", 1024, "fused", 0, 0.1, 0.1)
+    assert (cfg.time_budget, cfg.max_generations, cfg.assist_k0, cfg.start_velocity, cfg.anneal_gens) == \
+        (120.0, 500, 0.0, 0.0, 300)
+    assert cfg == es.Config()
+    cfg, backend, seed = es.parse_args(["--task", "legged4", "--pop", "256", "--backend", "mlx", "--seed", "3",
+                                        "--assist", "20", "--start-velocity", "0.3", "--anneal", "100",
+                                        "--lr", "0.05", "--sigma", "0.03", "--time-budget", "9",
+                                        "--max-generations", "7"])
+    assert backend == "loop" and seed == 3
+    assert (cfg.task, cfg.pop, cfg.assist_k0, cfg.start_velocity, cfg.anneal_gens) == ("legged4", 256, 20.0, 0.3, 100)
+    assert (cfg.lr, cfg.sigma, cfg.time_budget, cfg.max_generations) == (0.05, 0.03, 9.0, 7)
+    assert es.parse_args(["--backend", "seeded"])[1] == "seeded"
+    for name in ("metal", "mlx", "fused", "loop", "seeded"):
+        assert es.BACKEND_ALIASES.get(name, name) in es.BACKENDS
