@@ -56,3 +56,22 @@ def test_legged_rollout_traffic_is_tabulated():
     tabulated = {float(m) for m in re.findall(r"\d\.\d{4}e1\d", text)}
     for key, b in c["LEGGED_ROLLOUT_TRAFFIC"].items():
         assert float(f"{b:.4e}") in tabulated, (key, b)
+
+
+def test_cartpole_trace_matches_the_kernel_sources():
+    """CARTPOLE_TRACE_NS describes the build whose sources hash to CARTPOLE_TRACE_SOURCE_SHA;
+    a change to the CartPole kernel or the shared device header fails here until the kernel is
+    traced again (bench.py meanwhile reports its HIP-event figure as `frac`)."""
+    import hashlib
+
+    tree = ast.parse((ROOT / "bench.py").read_text())
+    consts = {}
+    for node in tree.body:
+        if isinstance(node, ast.Assign) and len(node.targets) == 1 and isinstance(node.targets[0], ast.Name):
+            if node.targets[0].id in ("CARTPOLE_TRACE_SOURCE_SHA", "CARTPOLE_TRACE_SOURCES"):
+                consts[node.targets[0].id] = ast.literal_eval(node.value)
+    h = hashlib.sha256()
+    for rel in consts["CARTPOLE_TRACE_SOURCES"]:
+        h.update((ROOT / rel).read_bytes())
+    assert h.hexdigest()[:16] == consts["CARTPOLE_TRACE_SOURCE_SHA"]
+    assert consts["CARTPOLE_TRACE_SOURCE_SHA"] in profile("cartpole_step_n262144.md")
