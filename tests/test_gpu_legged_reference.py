@@ -24,7 +24,7 @@ from test_oracle_legged import legged_states
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-LEGGED = [(c, s, 0) for c in (1, 2, 4) for s in (4, 8, 16)] + [(4, 8, 20)]
+LEGGED = [(c, s, 0) for c in (1, 2, 4) for s in (4, 8, 16)] + [(4, 8, 20)] + [(3, s, 0) for s in (4, 8, 16)]
 
 
 def to_np(t):
