@@ -255,3 +255,34 @@ def test_config4_population_matches_oracle(dev, c, iters):
     np.testing.assert_array_equal(to_np(sk), es_)
     np.testing.assert_array_equal(to_np(fk), ef)
     assert es_.min() < es_.max()
+
+
+@pytest.mark.parametrize("c", [2, 4])
+def test_horizon_1000_against_oracle(dev, c):
+    """The whole config-4 horizon at small P: 256 members of the benchmark's population
+    (H = 64, sigma 0.03 around theta0 = 0.1 N(0, 1), S = 8) with a torso-assist spring of 5,
+    so that some members stand for all 1,000 steps. After the first 32-step chunk the
+    survivors run in the group tail (16 lanes per member) to the end of their episodes; the
+    drop-in rollout and the seeded rollout each equal the oracle's fused restatement member
+    for member."""
+    from hipenvs import legged_rollout
+    from oracle import es_noise as oen
+
+    p, hidden, horizon, assist = 256, 64, 1000, 5.0
+    d = legged_rollout.n_params(hidden, c)
+    theta = (np.random.default_rng(77 + c).standard_normal(d) * 0.1).astype(np.float32)
+    pop = oen.perturb(theta, p, 91, 0.03)
+    state = olg.Legged(c).reset(p, seed=13)
+    print(f"horizon 1000 c={c}: oracle", flush=True)
+    ef, es_ = olg.rollout_fused(state, pop, hidden, horizon, c, iters=8, assist=assist)
+    assert (es_ >= horizon).sum() >= 4 and es_.min() < 32  # members in the first chunk only and to the end
+    st = torch.from_numpy(state).to(dev)
+    print(f"horizon 1000 c={c}: drop-in rollout", flush=True)
+    fk, sk = legged_rollout.rollout(st, torch.from_numpy(pop).to(dev), hidden, horizon, c, assist=assist)
+    np.testing.assert_array_equal(to_np(sk), es_)
+    np.testing.assert_array_equal(to_np(fk), ef)
+    print(f"horizon 1000 c={c}: seeded rollout", flush=True)
+    fs, ss = legged_rollout.rollout_seeded(st, torch.from_numpy(theta).to(dev), 91, 0.03, hidden, horizon, c,
+                                           assist=assist)
+    np.testing.assert_array_equal(to_np(ss), es_)
+    np.testing.assert_array_equal(to_np(fs), ef)

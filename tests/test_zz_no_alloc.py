@@ -101,3 +101,62 @@ def test_shapes_beyond_the_static_array_are_rejected(dev):
     theta_np, ranks_np, theta, ranks = case(dev, 2049, 64, 3)
     got = static(theta, ranks, 2049, 64, 3, 0.1, 0.1)
     np.testing.assert_array_equal(to_np(got), oen.update(theta_np, ranks_np, 3, 0.1, 0.1))
+
+
+CAPTURE_CHILD = r"""
+import sys
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import numpy as np
+import torch
+from hipenvs import _lib
+
+dev = torch.device("cuda", 0)
+d, p, seed, sigma, lr = 1676, 8192, 17, 0.03, 0.1
+rng = np.random.default_rng(seed)
+theta = torch.from_numpy((rng.standard_normal(d) * 0.1).astype(np.float32)).to(dev)
+ranks = torch.from_numpy(((np.argsort(np.argsort(rng.standard_normal(p), kind="stable"), kind="stable")
+                           / (p - 1)) - 0.5).astype(np.float32)).to(dev)
+out = torch.zeros_like(theta)
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+side = torch.cuda.Stream(device=dev)
+side.wait_stream(torch.cuda.current_stream(dev))
+with torch.cuda.stream(side):
+    with torch.cuda.graph(g, stream=side):
+        # the library's first call on this device: its static array's address is looked up here
+        rc = _lib.lib().hipenvs_es_update_static(_lib.ptr(theta), _lib.ptr(ranks), d, p, _lib.u32(seed), sigma, lr,
+                                                 _lib.ptr(out), _lib.stream_of(dev))
+torch.cuda.synchronize()
+print("captured, status", rc, flush=True)
+assert rc == _lib.OK, rc
+nbytes = _lib.lib().hipenvs_es_update_workspace_bytes(d, p)
+ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+want = torch.empty_like(theta)
+_lib.call("hipenvs_es_update", _lib.ptr(theta), _lib.ptr(ranks), d, p, _lib.u32(seed), sigma, lr, _lib.ptr(want),
+          _lib.ptr(ws), nbytes, _lib.stream_of(dev))
+torch.cuda.synchronize()
+for r in range(3):
+    out.fill_(float(r + 7))               # eager work between replays
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), f"replay {r} differs from hipenvs_es_update"
+    print(f"replay {r} equal", flush=True)
+print("capture ok", flush=True)
+"""
+
+
+def test_first_call_under_graph_capture(dev):
+    """A fresh process whose first call of the library on the device is made under HIP graph
+    capture (torch.cuda.graph, global capture mode): the static array's address is looked up
+    inside the capture, the captured update is replayed three times with eager work and
+    synchronisations between the replays, and every replay equals hipenvs_es_update's result."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    print("no-alloc update under graph capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", CAPTURE_CHILD, str(root), str(root / "metal-rl-envs_amd")],
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "capture ok" in r.stdout, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
