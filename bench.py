@@ -100,7 +100,7 @@ CARTPOLE_BYTES = 41
 # profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
 CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
 ABA_TRAFFIC = {4: 4649746, 16: 17437438, 64: 99818014}
-ABA_RK4_TRAFFIC = {}
+ABA_RK4_TRAFFIC = {4: 5102694, 16: 18511667, 32: 37387878, 64: 405806592}  # profiles/aba_rk4_n65536.md
 # The reference's articulated-body kernel (RK4, eval every 32) at N = 65,536 on its M3 Pro,
 # results/aba.csv:137,222,307,392,460 (K = 4, 8, 16, 32, 64).
 ABA_RK4_REFERENCE = {4: 450437382, 8: 184284347, 16: 68215640, 32: 17807725, 64: 3961767}
@@ -460,32 +460,44 @@ def cpu_rate_cartpole(n, seconds):
             return n * steps / el
 
 
-def sweep(dev, steps0, k, out_path, cpu_seconds=0.25):
+def sweep(dev, steps0, k, out_path, cpu_seconds=0.25, region_seconds=0.0):
     """Config-1 sweep: single-step and K-fused rates at N = 2^0..2^20 (and 2^22, 2^24), with the
     numpy rate at each N unless cpu_seconds is 0; the crossover is the first N where the
-    single-step GPU rate passes numpy's."""
+    single-step GPU rate passes numpy's. Every form is a HIP graph of `steps0` iterations
+    (128 past 2^20), replayed back to back in 3 timed regions of about `region_seconds` (at
+    least one replay each): the step alone on pre-drawn actions, the device sampler + step per
+    iteration (the reference's rule), and the K-fused step with in-kernel or array actions."""
     rows = []
     for e in list(range(0, 21)) + [22, 24]:
         n = 1 << e
         steps = steps0 if n <= (1 << 20) else 128  # keep the (steps, N) buffers a few GB
         run = CartPoleRun(n, steps, dev)
-        w1, ev1 = time_replay(run.graph_single(), 3)
-        wk, _ = time_replay(run.graph_fused(k, False), 3)
-        wka, _ = time_replay(run.graph_fused(k, True), 3)
-        launch = ev1 / steps
-        row = dict(n=n, steps=steps, single=n * steps / w1, fused_inkernel=n * steps / wk, fused_array=n * steps / wka,
-                   launch_us=launch * 1e6, single_gbs=CARTPOLE_BYTES * n / launch / 1e9)
+        g1 = run.graph_single()
+        reps = replays_for(g1, region_seconds) if region_seconds > 0 else 1
+        w1, ev1 = time_replay(g1, 3, reps)
+        ws, _ = time_replay(run.graph_sampled(), 3, reps)
+        wk, _ = time_replay(run.graph_fused(k, False), 3, reps)
+        wka, _ = time_replay(run.graph_fused(k, True), 3, reps)
+        its = steps * reps
+        launch = ev1 / its
+        row = dict(n=n, steps=steps, replays=reps, single=n * its / w1, sampled=n * its / ws,
+                   fused_inkernel=n * its / wk, fused_array=n * its / wka, launch_us=launch * 1e6,
+                   single_gbs=CARTPOLE_BYTES * n / launch / 1e9)
         if cpu_seconds > 0:
             row["numpy"] = cpu_rate_cartpole(n, cpu_seconds)
         rows.append(row)
-        log(f"N=2^{e:<2d} single {row['single']:>16,.0f}  fused(in-kernel) {row['fused_inkernel']:>16,.0f}  "
-            f"fused(array) {row['fused_array']:>16,.0f} env-steps/s  launch {row['launch_us']:7.2f} us "
-            f"{row['single_gbs']:8.1f} GB/s" + (f"  numpy {row['numpy']:>14,.0f}" if "numpy" in row else ""))
-        del run
+        log(f"N=2^{e:<2d} single {row['single']:>16,.0f}  sampler+step {row['sampled']:>16,.0f}  fused(in-kernel) "
+            f"{row['fused_inkernel']:>16,.0f}  fused(array) {row['fused_array']:>16,.0f} env-steps/s  launch "
+            f"{row['launch_us']:7.2f} us {row['single_gbs']:8.1f} GB/s"
+            + (f"  numpy {row['numpy']:>14,.0f}" if "numpy" in row else ""))
+        del run, g1
     crossover = next((r["n"] for r in rows if "numpy" in r and r["single"] > r["numpy"]), None)
+    crossover_sampled = next((r["n"] for r in rows if "numpy" in r and r["sampled"] > r["numpy"]), None)
+    out = {"rows": rows, "crossover_n": crossover, "crossover_n_sampler_and_step": crossover_sampled,
+           "steps_per_graph": steps0, "numpy_seconds_per_n": cpu_seconds}
     if out_path:
-        Path(out_path).write_text(json.dumps({"rows": rows, "crossover_n": crossover}, indent=1))
-    return {"rows": rows, "crossover_n": crossover}
+        Path(out_path).write_text(json.dumps(out, indent=1))
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -562,6 +574,8 @@ ALIVE_AT = (32, 64, 96, 128, 160, 192, 224, 256, 512, 999)
 
 
 def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
+    import torch
+
     from hipenvs import legged, legged_rollout
 
     hidden, p, horizon = 64, args.legged_n, args.legged_horizon
@@ -599,6 +613,28 @@ def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
             f"weights read at {rec['weight_stream_gbs']:.0f} GB/s")
         log(f"  alive after t steps: {', '.join(f'{t}: {n:,}' for t, n in alive.items() if t in ALIVE_AT)}; "
             f"member-steps in the first 32 steps: {alive['steps_in_first_32']:,}")
+    # the drop-in call with the reference's (P, D) rows: the module transposes them into the
+    # columns the chunked schedule reads (one 4 P D-byte copy), inside the timed call
+    walls, evs = [], []
+    for _ in range(args.repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        fit, steps = legged_rollout.rollout(state, theta, hidden, horizon, c, iters=8)
+        end.record()
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        evs.append(start.elapsed_time(end) / 1e3)
+    taken = float(steps.double().sum().item())
+    cols_rec = out["by_sweeps"].get("8")
+    out["drop_in_rows_s8"] = {"env_steps_per_s": taken / statistics.median(walls), "wall_s": statistics.median(walls),
+                              "kernel_event_s": statistics.median(evs),
+                              "transpose_bytes": 2 * 4 * d * p,
+                              "same_steps_as_columns": cols_rec is None or taken == cols_rec["steps_taken"]}
+    log(f"legged{c} drop-in rows call (transpose included), S=8: {taken / statistics.median(walls):,.0f} env-steps/s, "
+        f"{statistics.median(evs) * 1e3:.1f} ms")
+    del fit, steps
     if c == 4:
         wall, ev, taken, _ = time_rollout(state, theta, hidden, horizon, c, 8, "rows", 1)
         out["static_rows_s8_env_steps_per_s"] = taken / wall
@@ -943,6 +979,59 @@ def bench_aba_rk4(dev, steps=64, n=65536, ks=(4, 16, 32, 64), region_seconds=0.1
     return out
 
 
+# The reference's legged step (its chained kernel, eval every 32) at N = 65,536 on its M3 Pro
+# by Gauss-Seidel sweeps, README.md:1605-1612.
+LEGGED_STEP_REFERENCE = {2: {1: 148587531, 2: 130199428, 4: 130241539, 8: 112607332, 16: 85876189, 32: 58376177},
+                         4: {1: 27656704, 2: 27492110, 4: 26196758, 8: 24300548, 16: 21181268, 32: 17752265}}
+
+
+def bench_legged_step_sweep(dev, steps=200, n=65536, region_seconds=0.05):
+    """The reference's price list of the legged step by sweeps (README.md:1605-1612): the
+    float32 step at C = 2 and 4, S = 1/2/4/8/16/32, N = 65,536 from the stand reset, every
+    iteration drawing uniform actions in [0, 3^C) on the device and stepping, `steps`
+    iterations per HIP graph replayed back to back."""
+    import torch
+
+    from hipenvs import _lib, legged
+
+    P = _lib.ptr
+    fn = _lib.lib().hipenvs_legged_step
+    sampler = _lib.lib().hipenvs_sample_actions
+    out = {}
+    for c in (2, 4):
+        body_ = legged.Legged(c, 8)
+        rows = 2 * (3 + c)
+        stand = body_.stand_on(dev)
+        reward = torch.empty(n, device=dev)
+        done = torch.empty(n, dtype=torch.bool, device=dev)
+        row = torch.empty(n, dtype=torch.int32, device=dev)
+        for s_ in (1, 2, 4, 8, 16, 32):
+            bufs = [body_.reset(n, seed=0, device=dev), torch.empty((rows, n), device=dev)]
+
+            def sampled(st, s_=s_, bufs=bufs):
+                for t in range(steps):
+                    rc = sampler(P(row), n, 3 ** c, 1 + t, st)
+                    if rc != 0:
+                        raise RuntimeError(f"hipenvs_sample_actions failed: {rc}")
+                    rc = fn(c, s_, 0.0, P(bufs[t % 2]), P(row), t + 1, P(stand), P(bufs[(t + 1) % 2]), P(reward),
+                            P(done), n, st)
+                    if rc != 0:
+                        raise RuntimeError(f"legged step failed: {rc}")
+
+            g = capture_graph(dev, sampled)
+            per_region = replays_for(g, region_seconds)
+            wall, ev = time_replay(g, 3, per_region)
+            its = steps * per_region
+            rate = n * its / wall
+            ref = LEGGED_STEP_REFERENCE[c][s_]
+            out[f"c{c}_s{s_}"] = {"n_envs": n, "env_steps_per_s": rate, "us_per_iteration": wall / its * 1e6,
+                                  "reference_m3pro_env_steps_per_s": ref}
+            log(f"legged C={c} step S={s_} N={n}: {rate:,.0f} env-steps/s (sampler + step, "
+                f"{wall / its * 1e6:.2f} us per iteration); reference M3 Pro {ref:,}")
+            del g, bufs
+    return out
+
+
 def bench_step_bodies(dev, steps=1000, n=65536, ks=(2, 4, 8, 16)):
     """The reference's remaining step modules: the mass-matrix K-link pendulum (RK4, actions
     drawn per step on the device) and the hopper, graph-replayed like the ABA step."""
@@ -1043,9 +1132,14 @@ def main():
             extra["cartpole_step_n1048576"] = bench_cartpole_at(1 << 20, args.steps, args.repeats, dev)
         extra["cartpole_step_n16777216"] = bench_cartpole_at(1 << 24, 64, args.repeats, dev)
         extra["cartpole_copy_floor"] = [copy_floor(m, args.steps, args.repeats, dev) for m in (args.n, 1 << 20)]
+        # config 1: the full sweep with --sweep; a bounded one (64 iterations per graph, regions of
+        # about 20 ms, 0.05 s of numpy per N) in the default run
         if args.sweep:
             extra["cartpole_sweep"] = sweep(dev, args.steps, args.fused_k, args.sweep_out,
                                             0.0 if args.skip_cpu else 0.25)
+        elif args.only is None:
+            extra["cartpole_sweep"] = sweep(dev, 64, args.fused_k, args.sweep_out, 0.0 if args.skip_cpu else 0.05,
+                                            region_seconds=0.02)
     if args.only in (None, "legged"):
         for c in (4, 2):
             legged = bench_legged(args, dev, c)
@@ -1064,6 +1158,7 @@ def main():
         extra["aba_rk4"] = bench_aba_rk4(dev)
         if args.only == "steps":
             extra["step_bodies"] = bench_step_bodies(dev)
+            extra["legged_step_sweeps"] = bench_legged_step_sweep(dev)
         print(json.dumps(extra), flush=True)
         return
     if args.only is None:
@@ -1091,6 +1186,7 @@ def main():
                 log(f"ABA K={k} numpy: {rate:,.0f} env-steps/s -> GPU {rec['speedup_vs_cpu']:,.0f}x")
         extra["aba_rk4"] = bench_aba_rk4(dev)
         extra["step_bodies"] = bench_step_bodies(dev)
+        extra["legged_step_sweeps"] = bench_legged_step_sweep(dev)
 
     cpu = None
     if not args.skip_cpu and args.only in (None, "cartpole"):

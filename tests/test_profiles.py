@@ -44,6 +44,9 @@ def test_aba_and_step_body_traffic_are_tabulated():
     aba = numbers(profile("aba_euler_n65536.md"))
     for b in c["ABA_TRAFFIC"].values():
         assert float(b) in aba, b
+    rk4 = numbers(profile("aba_rk4_n65536.md"))
+    for b in c["ABA_RK4_TRAFFIC"].values():
+        assert float(b) in rk4, b
     bodies = numbers(profile("step_bodies_and_evaluate.md"))
     for name, b in c["STEP_BODY_TRAFFIC"].items():
         assert float(b) in bodies, (name, b)
