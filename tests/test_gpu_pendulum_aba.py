@@ -162,6 +162,41 @@ def test_rk4_reference_benchmark_chain(dev, k):
     np.testing.assert_array_equal(to_np(s_dev), s_ref)
 
 
+def test_k64_past_32bit_offsets(dev):
+    """The staged K = 64 kernels address the (128, n) arrays with 32-bit byte offsets, so from
+    n = 4,194,304 (2 GiB per array) the RK4 and the Euler step take the generic kernels. One
+    step of each at n = 4,194,304 + 200 (random wide chains drawn on the device), checked
+    against the oracle on the first 256 columns, 64 in the middle and the last 456 (the
+    envs are independent, so the oracle steps only those columns)."""
+    from hipenvs import pendulum_aba
+
+    k, n = 64, (1 << 22) + 200
+    print(f"K = 64 past 32-bit offsets: n = {n}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(64)
+    state = torch.empty((2 * k, n), device=dev)
+    state[:k].uniform_(-np.pi, np.pi, generator=g)
+    state[k:].uniform_(-1.0, 1.0, generator=g)
+    cols = np.concatenate([np.arange(256), np.arange(n // 2, n // 2 + 64), np.arange(n - 456, n)])
+    cols_dev = torch.from_numpy(cols).to(dev)
+    sub = to_np(state[:, cols_dev])
+    action = np.random.default_rng(5).integers(0, 3, n).astype(np.int32)
+    torque = np.random.default_rng(6).uniform(-1, 1, n).astype(np.float32)
+    p = pendulum_aba.Pendulum(k)
+    p.reseed(20)
+    ns, rew, done = p.step(state, torch.from_numpy(action).to(dev))
+    ens, erew, edone = oaba.Pendulum(k).step(sub, action[cols], seed=21)
+    assert not edone.any()  # the oracle's resets are keyed by column, so none may occur here
+    np.testing.assert_array_equal(to_np(ns[:, cols_dev]), ens)
+    np.testing.assert_array_equal(to_np(done[cols_dev]), edone)
+    del ns
+    p.reseed(30)
+    ns, rew, done = p.step_euler(state, torch.from_numpy(torque).to(dev))
+    ens, erew, edone = oaba.Pendulum(k).step_euler(sub, torque[cols], seed=31)
+    assert not edone.any()
+    np.testing.assert_array_equal(to_np(ns[:, cols_dev]), ens)
+    np.testing.assert_array_equal(to_np(done[cols_dev]), edone)
+
+
 def near_rest_states(k, seed):
     """Angles U[-0.38, 0.38] (every joint angle and every angle within 0.78 of zero), zero
     velocities, in six waves of 64 envs: waves 0 and 1 stay within the bound (wave 1 with one
