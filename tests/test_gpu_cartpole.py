@@ -57,6 +57,25 @@ def test_sample_actions_and_reset_match_the_counter_rng(dev):
         assert_same_floats(to_np(s), oc.reset(n, seed=12))
 
 
+@pytest.mark.parametrize("offset", [0, 1, 2, 3])
+def test_sample_actions_into_rows_at_any_alignment(dev, offset):
+    """The sampler writes several consecutive envs per thread, as 16-byte vectors where the
+    row is 16-byte aligned: rows at every 4-byte offset (out = a slice of a larger buffer),
+    with lengths on and off multiples of 16, each equal to the counter RNG's draws and with
+    the elements around the row untouched."""
+    from hipenvs import cartpole
+
+    for n in (1, 7, 16, 33, 262_144 + 5):
+        buf = torch.full((n + 8,), -7, dtype=torch.int32, device=dev)
+        out = buf[offset:offset + n]
+        cartpole.sample_actions(n, seed=91, device=dev, out=out)
+        got = to_np(buf)
+        np.testing.assert_array_equal(got[offset:offset + n], rng.action_bits(91, n))
+        assert (got[:offset] == -7).all() and (got[offset + n:] == -7).all()
+        cartpole.sample_actions(n, seed=92, m=3, device=dev, out=out)
+        np.testing.assert_array_equal(to_np(out), rng.uniform_actions(92, n, 3))
+
+
 @pytest.mark.parametrize("n", [1, 3, 100, 4096, 4099])
 def test_step_matches_oracle_on_random_states(dev, n):
     """Random states in [-1, 1] (test_cartpole.py:33-37), sizes on and off multiples of the
