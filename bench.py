@@ -613,8 +613,8 @@ def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
             f"weights read at {rec['weight_stream_gbs']:.0f} GB/s")
         log(f"  alive after t steps: {', '.join(f'{t}: {n:,}' for t, n in alive.items() if t in ALIVE_AT)}; "
             f"member-steps in the first 32 steps: {alive['steps_in_first_32']:,}")
-    # the drop-in call with the reference's (P, D) rows: the module transposes them into the
-    # columns the chunked schedule reads (one 4 P D-byte copy), inside the timed call
+    # the drop-in call with the reference's (P, D) rows, which the first chunk reads directly
+    # (each lane its member's row) instead of the (D, P) columns above
     walls, evs = [], []
     for _ in range(args.repeats):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -630,9 +630,8 @@ def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
     cols_rec = out["by_sweeps"].get("8")
     out["drop_in_rows_s8"] = {"env_steps_per_s": taken / statistics.median(walls), "wall_s": statistics.median(walls),
                               "kernel_event_s": statistics.median(evs),
-                              "transpose_bytes": 2 * 4 * d * p,
                               "same_steps_as_columns": cols_rec is None or taken == cols_rec["steps_taken"]}
-    log(f"legged{c} drop-in rows call (transpose included), S=8: {taken / statistics.median(walls):,.0f} env-steps/s, "
+    log(f"legged{c} drop-in rows call, S=8: {taken / statistics.median(walls):,.0f} env-steps/s, "
         f"{statistics.median(evs) * 1e3:.1f} ms")
     del fit, steps
     if c == 4:

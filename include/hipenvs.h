@@ -255,6 +255,19 @@ int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, 
                                       float* fitness, float* steps, void* workspace, int64_t workspace_bytes,
                                       hipenvs_stream_t stream);
 
+/* hipenvs_legged_es_rollout_chunked on the caller's theta_rows (p, D) in
+ * es.unflatten's layout, the reference's own theta_pop (legged_rollout_metal.py:70-83,
+ * es.py:152-164), with no transpose: the first chunk reads each member's row front to
+ * back (16-byte vector loads, so theta_rows must be 16-byte aligned; HIPENVS_E_ARG
+ * otherwise) and fetches only live members' weights. The rows are addressed with 32-bit
+ * byte offsets: HIPENVS_E_UNSUPPORTED when p * D * 4 >= 2^31 (use the columns form).
+ * Results identical to hipenvs_legged_es_rollout_chunked on the transpose. */
+int hipenvs_legged_es_rollout_chunked_rows(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
+                                           const float* state, const float* theta_rows, int64_t p, int32_t horizon,
+                                           float alive_bonus, float fall_penalty, float height_gate, double assist,
+                                           float* fitness, float* steps, void* workspace, int64_t workspace_bytes,
+                                           hipenvs_stream_t stream);
+
 /* ---- Greedy evaluation of one policy ----------------------------------- */
 /* The reference's evaluate (es.py:308-322) steps n fresh envs with the mean
  * policy for `steps` steps through the env step and sums, per env,

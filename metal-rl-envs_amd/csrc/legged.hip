@@ -716,6 +716,109 @@ __device__ __forceinline__ void policy_torques(const float* __restrict__ w, int6
   }
 }
 
+// One member's row of the caller's (P, D) weights, read through a buffer resource over the
+// whole array: row i starts at byte i * D * 4 (a per-lane offset in one VGPR), and a
+// position within the row is a wave-uniform byte offset (an immediate, or a scalar past
+// 4 KB). With flat pointers the compiler had kept one 64-bit address per load batch alive
+// across the policy and spilled them (496 B/lane at two waves per SIMD). The row offset
+// passes through an empty asm statement where the reader is made (once per step), so the
+// loads, which read the same addresses every step, are not hoisted out of the step loop
+// into registers. Requires P * D * 4 < 2^31 (checked by the caller); a read past the
+// array returns 0.
+struct MemberRow {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t lane_bytes;
+  __device__ MemberRow(const float* base, int64_t total_floats, int64_t i, int d)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)(total_floats * 4), 0x00020000)),
+        lane_bytes((uint32_t)(i * d * 4)) {
+    asm volatile("" : "+v"(lane_bytes));
+  }
+  // floats [first, first + M) of the row into out, kV at a time (kV-float aligned)
+  template <int kV, int M>
+  __device__ __forceinline__ void load(int first, float* out) const {
+    static_assert(M % kV == 0, "whole vectors");
+#pragma unroll
+    for (int m = 0; m < M; m += kV) {
+      const int at = (first + m) * 4;
+      if constexpr (kV == 4) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)lane_bytes, at, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[m + e] = __uint_as_float(x[e]);
+      } else if constexpr (kV == 2) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rsrc, (int)lane_bytes, at, 0);
+        out[m] = __uint_as_float(x[0]);
+        out[m + 1] = __uint_as_float(x[1]);
+      } else {
+        out[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)lane_bytes, at, 0));
+      }
+    }
+  }
+};
+
+// Floats per vector load along a member's (P, D) row: row i starts at i * D floats, so a
+// 16-byte aligned base keeps every row 4-float aligned when 4 divides D (C = 4 at every
+// hidden size) and 2-float aligned when D is even (C = 2).
+template <int C, int HID>
+constexpr int kRowVec = ((5 + 2 * C) * HID + HID + HID * 3 * C + 3 * C) % 4 == 0   ? 4
+                        : ((5 + 2 * C) * HID + HID + HID * 3 * C + 3 * C) % 2 == 0 ? 2
+                                                                                  : 1;
+
+// policy_torques on the member's own row of the caller's (P, D) array, es.unflatten's
+// layout (es.py:152-164): w1 (OBS, HID) input-major, b1 (HID), w2 (HID, OUT), b2 (OUT).
+// The hidden sums run input-major: each unit's accumulator starts at its bias and adds
+// obs_k * w1[k][j] for k in order, then the heads add h_j * w2[j][o] for j in order, the
+// same operations in the same order per accumulator as policy_torques. A lane therefore
+// reads its row front to back in vectors, and a wave fetches only its live members' rows:
+// in the columns layout a 128-byte line holds one weight of 32 members and is fetched
+// while any of them lives. Each batch's loads (one input's HID weights, or eight hidden
+// units' heads) issue before their first use.
+template <int C, int HID>
+__device__ __forceinline__ void policy_torques_rows(const MemberRow& row, const float (&q)[3 + C],
+                                                    const float (&v)[3 + C], float (&tq)[C]) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  using F = FlatRows<OBS, HID, OUT>;
+  constexpr int kV = kRowVec<C, HID>;
+  float obs[OBS];
+#pragma unroll
+  for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
+#pragma unroll
+  for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
+  float s[HID];
+  row.load<kV, HID>(F::b1(0), s);
+#pragma unroll
+  for (int k = 0; k < OBS; ++k) {
+    float wk[HID];
+    row.load<kV, HID>(F::w1(k, 0), wk);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < HID; ++j) s[j] = s[j] + obs[k] * wk[j];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float logit[OUT];
+  row.load<(OUT % kV == 0 ? kV : 1), OUT>(F::b2(0), logit);
+  constexpr int kHeads = HID >= 8 ? 8 : HID;  // hidden units per batch of head weights
+#pragma unroll
+  for (int j0 = 0; j0 < HID; j0 += kHeads) {
+    float w2b[kHeads * OUT];
+    row.load<kV, kHeads * OUT>(F::w2(j0, 0), w2b);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kHeads; ++u) {
+      const float hj = det_tanh(s[j0 + u]);
+#pragma unroll
+      for (int o = 0; o < OUT; ++o) logit[o] = logit[o] + hj * w2b[u * OUT + o];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int leg = 0; leg < C; ++leg) {
+    float torque = -1.0f, best = logit[3 * leg];
+    if (logit[3 * leg + 1] > best) { torque = 0.0f; best = logit[3 * leg + 1]; }
+    if (logit[3 * leg + 2] > best) { torque = 1.0f; }
+    tq[leg] = torque * TORQUE;
+  }
+}
+
 // The group form of policy_torques for a compacted member (UnitRows tile, stride 64): lane g
 // of the G-lane group computes hidden units g, g + G, ...; lane o < 3C sums head o over all
 // hidden units in order; the group exchanges the hidden values and the logits through its
@@ -1263,7 +1366,8 @@ __global__ __launch_bounds__(64, G >= 8 ? 2 : 1) void rollout_group_chunk_kernel
                                  assist_damping, fitness, steps_out, xs_all, xh_all, xl_all, xd_all);
 }
 
-template <int C, int HID, bool kFirst>
+// kRows (first chunk only): theta0 is the caller's (P, D) rows instead of its (D, P) columns.
+template <int C, int HID, bool kFirst, bool kRows = false>
 __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_ROLLOUT_MIN_WAVES) void rollout_chunk_kernel(const float* __restrict__ state0,
                                                            const float* __restrict__ theta0, int64_t p,
                                                            Packed src, Packed dst, int64_t cap,
@@ -1302,12 +1406,18 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
         t = src.meta[cap + i];
       }
     }
-    // the caller's (D, p) columns in the first chunk; the set's tile of this wave after
-    const float* w = kFirst ? stheta + i : stheta + (base / kTile) * (int64_t)D * kTile + lane;
+    // the caller's (D, p) columns or (p, D) rows in the first chunk; the set's tile of this
+    // wave after
+    static_assert(kFirst || !kRows, "rows are the caller's layout, read by the first chunk only");
+    const float* w = kRows    ? stheta + i * (int64_t)D
+                     : kFirst ? stheta + i
+                              : stheta + (base / kTile) * (int64_t)D * kTile + lane;
     for (int32_t k = 0; k < chunk_steps; ++k) {
       if (!__any(live)) break;
       if (!live) continue;
-      if constexpr (kFirst) {
+      if constexpr (kRows) {
+        policy_torques_rows<C, HID>(MemberRow(stheta, p * (int64_t)D, i, D), q, v, tq);
+      } else if constexpr (kFirst) {
         policy_torques<C, HID>(w, src_stride, q, v, tq);
       } else {
         policy_torques<C, HID, UnitRows, kTile>(w, kTile, q, v, tq);
@@ -1351,7 +1461,9 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
         dst.meta[slot] = id;
         dst.meta[cap + slot] = t;
         float* wd = dst.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
-        if constexpr (kFirst)  // caller's FlatRows columns -> UnitRows tile
+        if constexpr (kRows)  // caller's FlatRows row -> UnitRows tile
+          copy_flat_to_units<OBS, HID, OUT>(wd, kTile, w, 1);
+        else if constexpr (kFirst)  // caller's FlatRows columns -> UnitRows tile
           copy_flat_to_units<OBS, HID, OUT>(wd, kTile, w, src_stride);
         else  // tile -> tile, same rows
           copy_rows(wd, kTile, w, kTile, D);
@@ -1476,8 +1588,8 @@ int launch_later_chunk(const float* state0, const float* theta0, int64_t p, cons
 template <int C, int HID>
 struct ChunkTag {};
 
-template <int C, int HID>
-int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32_t horizon, int iters,
+template <int C, int HID, bool kRows>
+int launch_chunked(const float* state, const float* theta0, int64_t p, int32_t horizon, int iters,
                    int32_t chunk_steps, float alive, float fall, float gate, double assist, float* fitness,
                    float* steps, void* workspace, hipStream_t s) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
@@ -1510,14 +1622,14 @@ int launch_chunked(const float* state, const float* theta_cols, int64_t p, int32
   // first chunk: the caller's arrays -> set 0
   hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, 0u);
   const GroupBounds gb = group_bounds<C>(p, cus);
-  hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true>), dim3((unsigned)needed), dim3(64), 0, s, state, theta_cols,
+  hipLaunchKernelGGL((rollout_chunk_kernel<C, HID, true, kRows>), dim3((unsigned)needed), dim3(64), 0, s, state, theta0,
                      p, set[1], set[0], cap, first_steps, horizon, iters, alive, fall, gate, af, ad, fitness, steps,
                      gb.group_max);
   int status = launch_status();
   int cur = 0;
   const int64_t grid = resident < needed ? resident : needed;
   for (int64_t done = first_steps; status == HIPENVS_OK && done < horizon; done += chunk_steps) {
-    status = launch_later_chunk<C, HID>(state, theta_cols, p, set[cur], set[1 - cur], cap, grid, gb, chunk_steps,
+    status = launch_later_chunk<C, HID>(state, theta0, p, set[cur], set[1 - cur], cap, grid, gb, chunk_steps,
                                         horizon, iters, alive, fall, gate, af, ad, fitness, steps, s);
     cur = 1 - cur;
   }
@@ -1602,18 +1714,29 @@ int launch_evaluate(int32_t hidden, const float* state, const float* theta, int6
   return launch_status();
 }
 
-template <int C>
-int dispatch_chunked(int32_t hidden, const float* state, const float* theta_cols, int64_t p, int32_t horizon,
-                     int iters, int32_t chunk_steps, float alive, float fall, float gate, double assist,
-                     float* fitness, float* steps, void* workspace, hipStream_t s) {
+template <int C, bool kRows>
+int dispatch_chunked_layout(int32_t hidden, const float* state, const float* theta0, int64_t p, int32_t horizon,
+                            int iters, int32_t chunk_steps, float alive, float fall, float gate, double assist,
+                            float* fitness, float* steps, void* workspace, hipStream_t s) {
   switch (hidden) {
-    case 4: return launch_chunked<C, 4>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
-    case 8: return launch_chunked<C, 8>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
-    case 16: return launch_chunked<C, 16>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
-    case 32: return launch_chunked<C, 32>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
-    case 64: return launch_chunked<C, 64>(state, theta_cols, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 4: return launch_chunked<C, 4, kRows>(state, theta0, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 8: return launch_chunked<C, 8, kRows>(state, theta0, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 16: return launch_chunked<C, 16, kRows>(state, theta0, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 32: return launch_chunked<C, 32, kRows>(state, theta0, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
+    case 64: return launch_chunked<C, 64, kRows>(state, theta0, p, horizon, iters, chunk_steps, alive, fall, gate, assist, fitness, steps, workspace, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
+}
+
+// The chunked rollout from the caller's (D, p) columns (rows false) or (p, D) rows (true).
+template <int C>
+int dispatch_chunked(bool rows, int32_t hidden, const float* state, const float* theta0, int64_t p, int32_t horizon,
+                     int iters, int32_t chunk_steps, float alive, float fall, float gate, double assist,
+                     float* fitness, float* steps, void* workspace, hipStream_t s) {
+  return rows ? dispatch_chunked_layout<C, true>(hidden, state, theta0, p, horizon, iters, chunk_steps, alive, fall,
+                                                 gate, assist, fitness, steps, workspace, s)
+              : dispatch_chunked_layout<C, false>(hidden, state, theta0, p, horizon, iters, chunk_steps, alive, fall,
+                                                  gate, assist, fitness, steps, workspace, s);
 }
 
 template <int C>
@@ -1718,28 +1841,52 @@ extern "C" int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t 
   return 2 * (2 * n + d + 4) * lg::round_to_tile(p) * 4 + 64;
 }
 
+namespace {
+int legged_chunked(bool rows, int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps, const float* state,
+                   const float* theta0, int64_t p, int32_t horizon, float alive_bonus, float fall_penalty,
+                   float height_gate, double assist, float* fitness, float* steps, void* workspace,
+                   int64_t workspace_bytes, hipenvs_stream_t stream) {
+  if (p < 0 || horizon < 0 || iters < 0 || iters > kMaxIters || chunk_steps < 1 || p > 0x7fffffffLL ||
+      (p > 0 && (!state || !theta0 || !fitness || !steps || !workspace)))
+    return HIPENVS_E_ARG;
+  if (rows && ((uintptr_t)theta0 & 15u) != 0) return HIPENVS_E_ARG;  // rows are read as 16-byte vectors
+  if (p == 0) return HIPENVS_OK;
+  const int64_t need = hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p);
+  if (need < 0) return HIPENVS_E_UNSUPPORTED;
+  // the rows are read through a buffer resource with 32-bit byte offsets
+  const int64_t d = (5 + 2 * (int64_t)c) * hidden + hidden + hidden * 3 * (int64_t)c + 3 * (int64_t)c;
+  if (rows && p * d * 4 >= ((int64_t)1 << 31)) return HIPENVS_E_UNSUPPORTED;
+  if (workspace_bytes < need) return HIPENVS_E_ARG;
+  if (horizon == 0)  // nothing to step: every member scores 0 in 0 steps
+    return hipenvs_legged_es_rollout(c, hidden, iters, rows ? 0 : 1, state, theta0, p, 0, alive_bonus, fall_penalty,
+                                     height_gate, assist, fitness, steps, stream);
+  hipStream_t s = as_stream(stream);
+  switch (c) {
+    case 1: return lg::dispatch_chunked<1>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 2: return lg::dispatch_chunked<2>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 4: return lg::dispatch_chunked<4>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    default: return HIPENVS_E_UNSUPPORTED;
+  }
+}
+}  // namespace
+
 extern "C" int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
                                                  const float* state, const float* theta_cols, int64_t p,
                                                  int32_t horizon, float alive_bonus, float fall_penalty,
                                                  float height_gate, double assist, float* fitness, float* steps,
                                                  void* workspace, int64_t workspace_bytes, hipenvs_stream_t stream) {
-  if (p < 0 || horizon < 0 || iters < 0 || iters > kMaxIters || chunk_steps < 1 || p > 0x7fffffffLL ||
-      (p > 0 && (!state || !theta_cols || !fitness || !steps || !workspace)))
-    return HIPENVS_E_ARG;
-  if (p == 0) return HIPENVS_OK;
-  const int64_t need = hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p);
-  if (need < 0) return HIPENVS_E_UNSUPPORTED;
-  if (workspace_bytes < need) return HIPENVS_E_ARG;
-  if (horizon == 0)  // nothing to step: every member scores 0 in 0 steps
-    return hipenvs_legged_es_rollout(c, hidden, iters, 1, state, theta_cols, p, 0, alive_bonus, fall_penalty,
-                                     height_gate, assist, fitness, steps, stream);
-  hipStream_t s = as_stream(stream);
-  switch (c) {
-    case 1: return lg::dispatch_chunked<1>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
-    case 2: return lg::dispatch_chunked<2>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
-    case 4: return lg::dispatch_chunked<4>(hidden, state, theta_cols, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
-    default: return HIPENVS_E_UNSUPPORTED;
-  }
+  return legged_chunked(false, c, hidden, iters, chunk_steps, state, theta_cols, p, horizon, alive_bonus,
+                        fall_penalty, height_gate, assist, fitness, steps, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hipenvs_legged_es_rollout_chunked_rows(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
+                                                      const float* state, const float* theta_rows, int64_t p,
+                                                      int32_t horizon, float alive_bonus, float fall_penalty,
+                                                      float height_gate, double assist, float* fitness,
+                                                      float* steps, void* workspace, int64_t workspace_bytes,
+                                                      hipenvs_stream_t stream) {
+  return legged_chunked(true, c, hidden, iters, chunk_steps, state, theta_rows, p, horizon, alive_bonus,
+                        fall_penalty, height_gate, assist, fitness, steps, workspace, workspace_bytes, stream);
 }
 
 extern "C" int hipenvs_legged_es_rollout_seeded(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,

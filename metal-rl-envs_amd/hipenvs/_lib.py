@@ -52,6 +52,8 @@ SIGNATURES = {
                                   _P, _P, _P],
     "hipenvs_legged_es_rollout_chunked": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32,
                                           ctypes.c_double, _P, _P, _P, _I64, _P],
+    "hipenvs_legged_es_rollout_chunked_rows": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _F32, _F32, _F32,
+                                               ctypes.c_double, _P, _P, _P, _I64, _P],
     "hipenvs_pendulum_step": [_I32, _P, _P, _U32, _P, _P, _P, _I64, _P],
     "hipenvs_pendulum_accelerations": [_I32, _P, _P, _P, _I64, _P],
     "hipenvs_hopper_reset": [_P, _I64, _U32, _P],

@@ -15,9 +15,9 @@ Additions: ``iters`` (the reference fixes ITERS = 8 at build time) and
   the survivors of each chunk (state, accumulators, weights) are packed into a
   dense column buffer before the next. Episode lengths are heavy-tailed (mean
   ~43 steps at the benchmark's shape while a few members last the whole
-  horizon), so this keeps waves full. It reads the weights as columns (D, P);
-  ``theta_pop`` given as (P, D) rows is transposed first (one copy), and
-  ``theta_cols`` skips that copy.
+  horizon), so this keeps waves full. The first chunk reads ``theta_pop``'s
+  (P, D) rows directly (each lane its member's row, front to back), or the
+  (D, P) columns when they are given as ``theta_cols``.
 * "rows": one member per lane for the whole rollout, ``theta_pop`` (P, D).
 * "columns": one member per lane, ``theta_cols`` (D, P), the transpose, in which
   the 64 members of a wave load 256 contiguous bytes per weight.
@@ -59,11 +59,16 @@ def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=
     hidden = _lib.check_hidden(hidden)
     horizon = _lib.check_horizon(horizon)
     d = n_params(hidden, c)
-    if schedule == "chunked":
-        if theta_cols is None:
-            theta_cols = _lib.check_theta(theta_pop, p, d, state.device).T.contiguous()
+    rows = schedule == "chunked" and theta_cols is None
+    if rows:
+        theta_pop = _lib.check_theta(theta_pop, p, d, state.device)
+        if p * d * 4 >= 1 << 31:  # past the rows form's 32-bit offsets: the columns form on the transpose
+            rows, theta_cols = False, theta_pop.T.contiguous()
+        elif theta_pop.data_ptr() % 16:  # the first chunk reads rows as 16-byte vectors
+            theta_pop = theta_pop.clone()
+    if schedule == "chunked" and not rows:
         theta_pop = _lib.check_theta(theta_cols, d, p, state.device, "theta_cols")
-    else:
+    elif not rows:
         shape = (d, p) if schedule == "columns" else (p, d)
         theta_pop = _lib.check_theta(theta_pop, *shape, state.device)
     fitness = torch.empty(p, dtype=torch.float32, device=state.device)
@@ -74,9 +79,9 @@ def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=
         if schedule == "chunked":
             nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=state.device)
-            _lib.call("hipenvs_legged_es_rollout_chunked", c, hidden, int(iters), int(chunk_steps), _lib.ptr(state),
-                      _lib.ptr(theta_pop), p, horizon, *args, _lib.ptr(workspace), nbytes,
-                      _lib.stream_of(state.device))
+            entry = "hipenvs_legged_es_rollout_chunked_rows" if rows else "hipenvs_legged_es_rollout_chunked"
+            _lib.call(entry, c, hidden, int(iters), int(chunk_steps), _lib.ptr(state), _lib.ptr(theta_pop), p,
+                      horizon, *args, _lib.ptr(workspace), nbytes, _lib.stream_of(state.device))
         else:
             _lib.call("hipenvs_legged_es_rollout", c, hidden, int(iters), LAYOUTS[schedule], _lib.ptr(state),
                       _lib.ptr(theta_pop), p, horizon, *args, _lib.stream_of(state.device))

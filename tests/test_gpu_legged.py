@@ -113,7 +113,40 @@ def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon, iters):
     fr, sr = legged_rollout.rollout(st, th, hidden, horizon, c, schedule="rows", iters=iters)
     np.testing.assert_array_equal(to_np(fr), ef)
     np.testing.assert_array_equal(to_np(sr), es_)
+    # the chunked schedule from (D, P) columns as well as from the rows above
+    fq, sq = legged_rollout.rollout(st, None, hidden, horizon, c, iters=iters, theta_cols=th.T.contiguous())
+    np.testing.assert_array_equal(to_np(fq), ef)
+    np.testing.assert_array_equal(to_np(sq), es_)
     assert 1 <= es_.mean() <= horizon
+
+
+@pytest.mark.parametrize("c", [1, 2, 4])
+def test_chunked_rows_at_any_alignment_and_ragged_p(dev, c):
+    """The chunked schedule reading the caller's (P, D) rows in its first chunk: a population
+    that is a view 4 bytes into a larger buffer (copied to an aligned one by the module;
+    the C ABI itself refuses an unaligned pointer), and P off multiples of 64; equal to the
+    columns form and the one-lane static schedule."""
+    from hipenvs import _lib, legged_rollout
+
+    hidden, horizon = 64, 48
+    for p in (1, 63, 130):
+        d = legged_rollout.n_params(hidden, c)
+        theta = torch.from_numpy(_population(p, c, hidden, 0.3, 50 + p)).to(dev)
+        buf = torch.zeros(p * d + 4, device=dev)
+        buf[1:1 + p * d] = theta.reshape(-1)
+        view = buf[1:1 + p * d].view(p, d)
+        assert view.data_ptr() % 16 != 0
+        st = torch.from_numpy(olg.Legged(c).reset(p, seed=60 + p)).to(dev)
+        fr, sr = legged_rollout.rollout(st, view, hidden, horizon, c)
+        fc, sc = legged_rollout.rollout(st, None, hidden, horizon, c, theta_cols=theta.T.contiguous())
+        fs, ss = legged_rollout.rollout(st, theta, hidden, horizon, c, schedule="rows")
+        assert torch.equal(fr, fc) and torch.equal(sr, sc) and torch.equal(fr, fs) and torch.equal(sr, ss), (c, p)
+        nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        rc = _lib.lib().hipenvs_legged_es_rollout_chunked_rows(c, hidden, 8, 32, _lib.ptr(st), _lib.ptr(view), p,
+                                                              horizon, 1.0, 0.0, 0.0, 0.0, _lib.ptr(fr), _lib.ptr(sr),
+                                                              _lib.ptr(ws), nbytes, _lib.stream_of(dev))
+        assert rc == _lib.E_ARG
 
 
 def test_chunked_schedule_at_scale_equals_static(dev):
