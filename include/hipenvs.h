@@ -258,10 +258,10 @@ int hipenvs_legged_es_rollout_chunked(int32_t c, int32_t hidden, int32_t iters, 
 /* hipenvs_legged_es_rollout_chunked on the caller's theta_rows (p, D) in
  * es.unflatten's layout, the reference's own theta_pop (legged_rollout_metal.py:70-83,
  * es.py:152-164), with no transpose: the first chunk reads each member's row front to
- * back (16-byte vector loads, so theta_rows must be 16-byte aligned; HIPENVS_E_ARG
- * otherwise) and fetches only live members' weights. The rows are addressed with 32-bit
- * byte offsets: HIPENVS_E_UNSUPPORTED when p * D * 4 >= 2^31 (use the columns form).
- * Results identical to hipenvs_legged_es_rollout_chunked on the transpose. */
+ * back (16-byte loads at any 4-byte alignment; HIPENVS_E_ARG for a theta_rows that is not
+ * 4-byte aligned) and fetches only live members' weights. The rows are addressed with
+ * 32-bit byte offsets: HIPENVS_E_UNSUPPORTED when p * D * 4 >= 2^31 (use the columns
+ * form). Results identical to hipenvs_legged_es_rollout_chunked on the transpose. */
 int hipenvs_legged_es_rollout_chunked_rows(int32_t c, int32_t hidden, int32_t iters, int32_t chunk_steps,
                                            const float* state, const float* theta_rows, int64_t p, int32_t horizon,
                                            float alive_bonus, float fall_penalty, float height_gate, double assist,

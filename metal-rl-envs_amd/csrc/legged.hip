@@ -733,35 +733,27 @@ struct MemberRow {
         lane_bytes((uint32_t)(i * d * 4)) {
     asm volatile("" : "+v"(lane_bytes));
   }
-  // floats [first, first + M) of the row into out, kV at a time (kV-float aligned)
-  template <int kV, int M>
+  // floats [first, first + M) of the row into out: 16-byte loads, then one 8- or 4-byte load
+  // for a remainder. A row starts at any 4-byte boundary (D may be odd); the hardware serves
+  // dword-aligned 16-byte loads, which hipcc itself emits for 4-byte aligned float4 data.
+  template <int M>
   __device__ __forceinline__ void load(int first, float* out) const {
-    static_assert(M % kV == 0, "whole vectors");
 #pragma unroll
-    for (int m = 0; m < M; m += kV) {
-      const int at = (first + m) * 4;
-      if constexpr (kV == 4) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)lane_bytes, at, 0);
+    for (int m = 0; m + 4 <= M; m += 4) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)lane_bytes, (first + m) * 4, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) out[m + e] = __uint_as_float(x[e]);
-      } else if constexpr (kV == 2) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rsrc, (int)lane_bytes, at, 0);
-        out[m] = __uint_as_float(x[0]);
-        out[m + 1] = __uint_as_float(x[1]);
-      } else {
-        out[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)lane_bytes, at, 0));
-      }
+      for (int e = 0; e < 4; ++e) out[m + e] = __uint_as_float(x[e]);
     }
+    constexpr int m = M / 4 * 4;
+    if constexpr (M - m >= 2) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b64(rsrc, (int)lane_bytes, (first + m) * 4, 0);
+      out[m] = __uint_as_float(x[0]);
+      out[m + 1] = __uint_as_float(x[1]);
+    }
+    if constexpr ((M - m) % 2 == 1)
+      out[M - 1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)lane_bytes, (first + M - 1) * 4, 0));
   }
 };
-
-// Floats per vector load along a member's (P, D) row: row i starts at i * D floats, so a
-// 16-byte aligned base keeps every row 4-float aligned when 4 divides D (C = 4 at every
-// hidden size) and 2-float aligned when D is even (C = 2).
-template <int C, int HID>
-constexpr int kRowVec = ((5 + 2 * C) * HID + HID + HID * 3 * C + 3 * C) % 4 == 0   ? 4
-                        : ((5 + 2 * C) * HID + HID + HID * 3 * C + 3 * C) % 2 == 0 ? 2
-                                                                                  : 1;
 
 // policy_torques on the member's own row of the caller's (P, D) array, es.unflatten's
 // layout (es.py:152-164): w1 (OBS, HID) input-major, b1 (HID), w2 (HID, OUT), b2 (OUT).
@@ -777,30 +769,29 @@ __device__ __forceinline__ void policy_torques_rows(const MemberRow& row, const 
                                                     const float (&v)[3 + C], float (&tq)[C]) {
   constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
   using F = FlatRows<OBS, HID, OUT>;
-  constexpr int kV = kRowVec<C, HID>;
   float obs[OBS];
 #pragma unroll
   for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
 #pragma unroll
   for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
   float s[HID];
-  row.load<kV, HID>(F::b1(0), s);
+  row.load<HID>(F::b1(0), s);
 #pragma unroll
   for (int k = 0; k < OBS; ++k) {
     float wk[HID];
-    row.load<kV, HID>(F::w1(k, 0), wk);
+    row.load<HID>(F::w1(k, 0), wk);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < HID; ++j) s[j] = s[j] + obs[k] * wk[j];
     __builtin_amdgcn_sched_barrier(0);
   }
   float logit[OUT];
-  row.load<(OUT % kV == 0 ? kV : 1), OUT>(F::b2(0), logit);
+  row.load<OUT>(F::b2(0), logit);
   constexpr int kHeads = HID >= 8 ? 8 : HID;  // hidden units per batch of head weights
 #pragma unroll
   for (int j0 = 0; j0 < HID; j0 += kHeads) {
     float w2b[kHeads * OUT];
-    row.load<kV, kHeads * OUT>(F::w2(j0, 0), w2b);
+    row.load<kHeads * OUT>(F::w2(j0, 0), w2b);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kHeads; ++u) {
@@ -1849,7 +1840,7 @@ int legged_chunked(bool rows, int32_t c, int32_t hidden, int32_t iters, int32_t 
   if (p < 0 || horizon < 0 || iters < 0 || iters > kMaxIters || chunk_steps < 1 || p > 0x7fffffffLL ||
       (p > 0 && (!state || !theta0 || !fitness || !steps || !workspace)))
     return HIPENVS_E_ARG;
-  if (rows && ((uintptr_t)theta0 & 15u) != 0) return HIPENVS_E_ARG;  // rows are read as 16-byte vectors
+  if (rows && ((uintptr_t)theta0 & 3u) != 0) return HIPENVS_E_ARG;  // rows are read as dword-aligned vectors
   if (p == 0) return HIPENVS_OK;
   const int64_t need = hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p);
   if (need < 0) return HIPENVS_E_UNSUPPORTED;

@@ -64,8 +64,6 @@ def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=
         theta_pop = _lib.check_theta(theta_pop, p, d, state.device)
         if p * d * 4 >= 1 << 31:  # past the rows form's 32-bit offsets: the columns form on the transpose
             rows, theta_cols = False, theta_pop.T.contiguous()
-        elif theta_pop.data_ptr() % 16:  # the first chunk reads rows as 16-byte vectors
-            theta_pop = theta_pop.clone()
     if schedule == "chunked" and not rows:
         theta_pop = _lib.check_theta(theta_cols, d, p, state.device, "theta_cols")
     elif not rows:

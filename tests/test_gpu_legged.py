@@ -122,31 +122,34 @@ def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon, iters):
 
 @pytest.mark.parametrize("c", [1, 2, 4])
 def test_chunked_rows_at_any_alignment_and_ragged_p(dev, c):
-    """The chunked schedule reading the caller's (P, D) rows in its first chunk: a population
-    that is a view 4 bytes into a larger buffer (copied to an aligned one by the module;
-    the C ABI itself refuses an unaligned pointer), and P off multiples of 64; equal to the
-    columns form and the one-lane static schedule."""
+    """The chunked schedule reading the caller's (P, D) rows in its first chunk: populations
+    that are views 4, 8 and 12 bytes into a larger buffer (rows at every 4-byte alignment,
+    read in place through the C ABI), and P off multiples of 64; equal to the columns form
+    and the one-lane static schedule."""
     from hipenvs import _lib, legged_rollout
 
     hidden, horizon = 64, 48
-    for p in (1, 63, 130):
+    for p, off in ((1, 1), (63, 2), (130, 3), (130, 0)):
         d = legged_rollout.n_params(hidden, c)
         theta = torch.from_numpy(_population(p, c, hidden, 0.3, 50 + p)).to(dev)
         buf = torch.zeros(p * d + 4, device=dev)
-        buf[1:1 + p * d] = theta.reshape(-1)
-        view = buf[1:1 + p * d].view(p, d)
-        assert view.data_ptr() % 16 != 0
+        buf[off:off + p * d] = theta.reshape(-1)
+        view = buf[off:off + p * d].view(p, d)
+        assert view.data_ptr() % 16 == 4 * off
         st = torch.from_numpy(olg.Legged(c).reset(p, seed=60 + p)).to(dev)
         fr, sr = legged_rollout.rollout(st, view, hidden, horizon, c)
         fc, sc = legged_rollout.rollout(st, None, hidden, horizon, c, theta_cols=theta.T.contiguous())
         fs, ss = legged_rollout.rollout(st, theta, hidden, horizon, c, schedule="rows")
         assert torch.equal(fr, fc) and torch.equal(sr, sc) and torch.equal(fr, fs) and torch.equal(sr, ss), (c, p)
+        # the C ABI directly, on the unaligned view: the same results
         nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        fa, sa = torch.empty_like(fr), torch.empty_like(sr)
         rc = _lib.lib().hipenvs_legged_es_rollout_chunked_rows(c, hidden, 8, 32, _lib.ptr(st), _lib.ptr(view), p,
-                                                              horizon, 1.0, 0.0, 0.0, 0.0, _lib.ptr(fr), _lib.ptr(sr),
+                                                              horizon, 1.0, 0.0, 0.0, 0.0, _lib.ptr(fa), _lib.ptr(sa),
                                                               _lib.ptr(ws), nbytes, _lib.stream_of(dev))
-        assert rc == _lib.E_ARG
+        assert rc == 0
+        assert torch.equal(fa, fc) and torch.equal(sa, sc), (c, p, off)
 
 
 def test_chunked_schedule_at_scale_equals_static(dev):
