@@ -225,7 +225,7 @@ int hipenvs_legged_step_reference(int32_t c, int32_t iters, double assist, const
  * to `horizon` steps; fitness (p) = sum of ((v_x if y >= height_gate else 0) +
  * alive_bonus) until the first fall, minus fall_penalty at it; steps (p) = steps
  * taken including the falling one. layout 0: theta (p, D) rows in es.unflatten's
- * layout; layout 1: theta (D, p) columns. c in {1, 2, 4}, hidden in
+ * layout; layout 1: theta (D, p) columns. c in {1, 2, 3, 4}, hidden in
  * {4, 8, 16, 32, 64}, iters 0..4096.
  * Replaces the `legged_es_rollout` Metal kernel and legged_rollout_metal.rollout
  * (legged_rollout_metal.py:19-83), whose ITERS the reference fixes at 8. */
@@ -287,7 +287,7 @@ int hipenvs_cartpole_evaluate(const float* state, const float* theta, int64_t n,
 int hipenvs_acrobot_evaluate(const float* state, const float* theta, int64_t n, int32_t hidden, int32_t steps,
                              float* fitness, hipenvs_stream_t stream);
 
-/* Legged body with c in {1, 2, 4}, no assist: sum of ((v_x + 1) - 1) + eval_bonus
+/* Legged body with c in {1, 2, 3, 4}, no assist: sum of ((v_x + 1) - 1) + eval_bonus
  * while standing (the reference's legged tasks use eval_bonus 0: forward distance).
  * Replaces evaluate for the legged tasks (es.py:302-322, legged_np.py:114-121). */
 int hipenvs_legged_evaluate(int32_t c, int32_t hidden, int32_t iters, const float* state, const float* theta,

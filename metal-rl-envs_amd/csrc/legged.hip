@@ -608,6 +608,11 @@ __device__ __forceinline__ bool fallen(const float (&q)[3 + C]) {
 #ifndef LEGGED_FIRST_CHUNK_MIN_WAVES
 #define LEGGED_FIRST_CHUNK_MIN_WAVES 1
 #endif
+// Whether the first chunk's column base is made opaque to the compiler every step (see
+// rollout_chunk_kernel).
+#ifndef LEGGED_FIRST_CHUNK_OPAQUE_COLUMNS
+#define LEGGED_FIRST_CHUNK_OPAQUE_COLUMNS 1
+#endif
 // Whether the chunk kernels park the substep's M^-1 J^T columns in LDS during the
 // Gauss-Seidel sweeps (substep's kStage, 14 KB per single-wave workgroup at C = 4). The
 // sweeps hold the most registers; with the columns in LDS the C = 4 chunk kernels need about
@@ -1409,7 +1414,12 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
       if constexpr (kRows) {
         policy_torques_rows<C, HID>(MemberRow(stheta, p * (int64_t)D, i, D), q, v, tq);
       } else if constexpr (kFirst) {
-        policy_torques<C, HID>(w, src_stride, q, v, tq);
+        // the column base passes through an empty asm statement every step, so the loads
+        // (the same addresses each step) stay in the loop: at H = 4 the compiler had
+        // hoisted all 120 weights into registers and spilled 60 B/lane
+        const float* wk = w;
+        if constexpr (LEGGED_FIRST_CHUNK_OPAQUE_COLUMNS != 0) asm volatile("" : "+v"(wk));
+        policy_torques<C, HID>(wk, src_stride, q, v, tq);
       } else {
         policy_torques<C, HID, UnitRows, kTile>(w, kTile, q, v, tq);
       }
@@ -1818,13 +1828,14 @@ extern "C" int hipenvs_legged_es_rollout(int32_t c, int32_t hidden, int32_t iter
   switch (c) {
     case 1: return lg::dispatch_hidden<1>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
     case 2: return lg::dispatch_hidden<2>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
+    case 3: return lg::dispatch_hidden<3>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
     case 4: return lg::dispatch_hidden<4>(hidden, columns, state, theta, p, horizon, iters, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
 }
 
 extern "C" int64_t hipenvs_legged_es_rollout_workspace_bytes(int32_t c, int32_t hidden, int64_t p) {
-  if (p < 0 || (c != 1 && c != 2 && c != 4) || (hidden != 4 && hidden != 8 && hidden != 16 && hidden != 32 &&
+  if (p < 0 || c < 1 || c > 4 || (hidden != 4 && hidden != 8 && hidden != 16 && hidden != 32 &&
                                                 hidden != 64))
     return -1;
   const int64_t n = 3 + c, obs = 5 + 2 * c, out = 3 * c;
@@ -1855,6 +1866,7 @@ int legged_chunked(bool rows, int32_t c, int32_t hidden, int32_t iters, int32_t 
   switch (c) {
     case 1: return lg::dispatch_chunked<1>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 2: return lg::dispatch_chunked<2>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 3: return lg::dispatch_chunked<3>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 4: return lg::dispatch_chunked<4>(rows, hidden, state, theta0, p, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
@@ -1901,6 +1913,7 @@ extern "C" int hipenvs_legged_es_rollout_seeded(int32_t c, int32_t hidden, int32
   switch (c) {
     case 1: return lg::dispatch_chunked_seeded<1>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 2: return lg::dispatch_chunked_seeded<2>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
+    case 3: return lg::dispatch_chunked_seeded<3>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     case 4: return lg::dispatch_chunked_seeded<4>(hidden, state, theta, p, seed, sg, horizon, iters, chunk_steps, alive_bonus, fall_penalty, height_gate, assist, fitness, steps, workspace, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }
@@ -1916,6 +1929,7 @@ extern "C" int hipenvs_legged_evaluate(int32_t c, int32_t hidden, int32_t iters,
   switch (c) {
     case 1: return lg::launch_evaluate<1>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
     case 2: return lg::launch_evaluate<2>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
+    case 3: return lg::launch_evaluate<3>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
     case 4: return lg::launch_evaluate<4>(hidden, state, theta, n, steps, iters, eval_bonus, fitness, s);
     default: return HIPENVS_E_UNSUPPORTED;
   }

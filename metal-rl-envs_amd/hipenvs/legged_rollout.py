@@ -32,7 +32,7 @@ from . import _lib
 LAYOUTS = {"rows": 0, "columns": 1}
 SCHEDULES = ("chunked", "rows", "columns")
 CHUNK_STEPS = 32
-SUPPORTED_C = (1, 2, 4)
+SUPPORTED_C = (1, 2, 3, 4)
 
 
 def n_params(hidden, c):

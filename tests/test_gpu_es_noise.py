@@ -78,7 +78,7 @@ def test_cartpole_and_acrobot_seeded_rollouts(dev, p, hidden):
         assert expect.max().item() > 0
 
 
-@pytest.mark.parametrize("c,hidden,p", [(4, 64, 640), (4, 16, 20_000), (2, 32, 3000), (1, 8, 130)])
+@pytest.mark.parametrize("c,hidden,p", [(4, 64, 640), (4, 16, 20_000), (3, 64, 3000), (2, 32, 3000), (1, 8, 130)])
 def test_legged_seeded_rollout(dev, c, hidden, p):
     """Populations the group tail takes whole (640, 130, 3000 at or below 16 per CU) and one
     that runs compacted chunks first (20,000), with and without the assist spring."""

@@ -42,7 +42,7 @@ def test_cartpole_and_acrobot_evaluate_match_oracle(dev, n, hidden):
     assert not np.any(np.signbit(to_np(got)) & (to_np(got) == 0))  # no -0 scores
 
 
-@pytest.mark.parametrize("c,hidden", [(1, 8), (2, 16), (4, 64)])
+@pytest.mark.parametrize("c,hidden", [(1, 8), (2, 16), (3, 32), (4, 64)])
 def test_legged_evaluate_matches_oracle(dev, c, hidden):
     from hipenvs import legged, legged_rollout
 

@@ -94,7 +94,7 @@ def _population(p, c, hidden, scale, seed):
 
 @pytest.mark.parametrize("iters", [4, 8, 16])
 @pytest.mark.parametrize("c,hidden,p,horizon", [(1, 8, 128, 60), (2, 16, 256, 100), (2, 64, 96, 40),
-                                                 (4, 64, 96, 40)])
+                                                 (3, 32, 96, 40), (4, 64, 96, 40)])
 def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon, iters):
     """Every schedule at the benchmark's sweep counts S = 4, 8, 16, including the biped and
     the quadruped at H = 64."""
@@ -120,7 +120,7 @@ def test_rollout_matches_oracle_both_layouts(dev, c, hidden, p, horizon, iters):
     assert 1 <= es_.mean() <= horizon
 
 
-@pytest.mark.parametrize("c", [1, 2, 4])
+@pytest.mark.parametrize("c", [1, 2, 3, 4])
 def test_chunked_rows_at_any_alignment_and_ragged_p(dev, c):
     """The chunked schedule reading the caller's (P, D) rows in its first chunk: populations
     that are views 4, 8 and 12 bytes into a larger buffer (rows at every 4-byte alignment,
@@ -174,8 +174,8 @@ def test_chunked_schedule_at_scale_equals_static(dev):
     assert torch.equal(fq, fs) and torch.equal(sq, ss)
 
 
-@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (1, 64, 8), (2, 8, 8), (2, 32, 8), (4, 4, 8), (4, 64, 8),
-                                            (2, 64, 4), (2, 64, 16), (4, 64, 4), (4, 64, 16)])
+@pytest.mark.parametrize("c,hidden,iters", [(1, 4, 8), (1, 64, 8), (2, 8, 8), (2, 32, 8), (3, 16, 8), (3, 64, 8),
+                                            (4, 4, 8), (4, 64, 8), (2, 64, 4), (2, 64, 16), (4, 64, 4), (4, 64, 16)])
 def test_group_tail_equals_static(dev, c, hidden, iters):
     """Populations that the compacting schedule hands to its group tail (a lane group per
     member) after the first chunk, at every leg count and hidden width the group code
@@ -196,9 +196,9 @@ def test_group_tail_equals_static(dev, c, hidden, iters):
         assert ss.max().item() > 8  # members outlived the first chunk
 
 
-@pytest.mark.parametrize("c,hidden,iters,above", [(1, 4, 8, 8), (2, 32, 8, 8), (4, 64, 8, 8), (2, 64, 4, 8),
-                                                  (4, 64, 16, 8), (4, 4, 8, 8), (4, 32, 8, 8), (4, 64, 8, 44),
-                                                  (2, 64, 8, 28)])
+@pytest.mark.parametrize("c,hidden,iters,above", [(1, 4, 8, 8), (2, 32, 8, 8), (3, 64, 8, 8), (4, 64, 8, 8),
+                                                  (2, 64, 4, 8), (4, 64, 16, 8), (4, 4, 8, 8), (4, 32, 8, 8),
+                                                  (4, 64, 8, 44), (2, 64, 8, 28)])
 def test_group_chunk_equals_static(dev, c, hidden, iters, above):
     """Populations `above` members per CU over the group tail's bound (16 per CU at C = 4, 32
     at C <= 2, where the tail runs two waves per SIMD), within 64 per CU. Later chunks run in

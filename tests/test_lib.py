@@ -36,7 +36,11 @@ def test_python_binding_covers_the_header():
     status_fns = set(declared_functions()) - {"hipenvs_version", "hipenvs_last_hip_error"} - set(_lib.VALUE_SIGNATURES)
     assert status_fns == set(_lib.SIGNATURES)
     assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(4, 64, 1000) > 1000 * 1676 * 4
-    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(3, 64, 1000) == -1
+    # two sets of 1,024 slots x (2 x 6 state rows + D = 1,353 weights + 4), plus the counters
+    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(3, 64, 1000) == 2 * (12 + 1353 + 4) * 1024 * 4 + 64
+    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(5, 64, 1000) == -1
+    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(0, 64, 1000) == -1
+    assert _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(4, 12, 1000) == -1
     assert _lib.version().startswith("hipenvs ")
     assert _lib.lib().hipenvs_last_hip_error() == 0
 
