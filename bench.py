@@ -108,8 +108,8 @@ STEP_BODY_TRAFFIC = {"pendulum_k2": 2833253, "pendulum_k4": 5104345, "pendulum_k
                      "pendulum_k16": 19185779, "hopper": 4889324, "acrobot": 10906005, "legged4_s8": 8227360,
                      "legged4_s8_reference": 16402468}
 # per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 103070000000, (4, 8): 116230000000, (4, 16): 125430000000,
-                          (2, 4): 45910000000, (2, 8): 48832000000, (2, 16): 65404000000}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 103070300949, (4, 8): 116239504630, (4, 16): 125435736933,
+                          (2, 4): 45783718429, (2, 8): 48714675453, (2, 16): 65271232788}
 
 
 def log(msg):

@@ -1182,15 +1182,23 @@ constexpr int kTile = 64;
 __host__ __device__ constexpr int64_t round_to_tile(int64_t n) { return (n + kTile - 1) / kTile * kTile; }
 
 // The tail of a rollout: once at most wide_max members survive (about one wave per SIMD in
-// this form), each compacted member gets a group of kGroupLanes lanes and runs to the end
-// of its episode (policy_group, substep_exact_group), kGroupMembers members per wave. The
+// this form), each compacted member gets a group of kTailLanes<C> lanes and runs to the end
+// of its episode (policy_group, substep_exact_group), kTailMembers<C> members per wave. The
 // group shortens one member's step, which is what bounds the tail. Results are those of the
 // one-lane schedule, bit for bit.
-constexpr int kGroupLanes = 16;
-#ifndef LEGGED_TAIL_MEMBERS_PER_CU
-// survivors per CU at the switch per tail wave on each SIMD (4-member waves; x kTailWaves<C>)
-#define LEGGED_TAIL_MEMBERS_PER_CU 16
+// At C <= 2 every lane role fits in 8 lanes (2C + 1 solves, C^2 Delassus blocks, 3C heads),
+// so eight members share a wave and the tail runs one wave per SIMD from 32 survivors per CU.
+// With 16 lanes it ran two 4-member waves per SIMD from the same count, which share the
+// SIMD's issue to the end of the horizon: biped ES rollout at N = 262,144 19.6 -> 17.9,
+// 23.8 -> 21.7 and 32.4 -> 30.2 ms at 4, 8 and 16 sweeps. Eight lanes at two waves per SIMD
+// from 64 per CU (LEGGED_SMALL_TAIL_WAVES 2, no group chunks) took 20.6, 25.5 and 35.2 ms.
+#ifndef LEGGED_SMALL_TAIL_LANES
+#define LEGGED_SMALL_TAIL_LANES 8
 #endif
+template <int C>
+constexpr int kTailLanes = C <= 2 ? LEGGED_SMALL_TAIL_LANES : 16;
+template <int C>
+constexpr int kTailMembers = 64 / kTailLanes<C>;
 // Above the tail's bound and up to this many survivors per CU, a chunk runs in the group form
 // (rollout_group_chunk_kernel) instead of one member per lane, with LEGGED_GROUP_CHUNK_LANES
 // lanes per member. With the split Gauss-Seidel sweeps (a 4-lane group broadcasts with one
@@ -1205,15 +1213,17 @@ constexpr int kGroupLanes = 16;
 #define LEGGED_GROUP_CHUNK_LANES 4
 #endif
 constexpr int kChunkGroupLanes = LEGGED_GROUP_CHUNK_LANES;
-constexpr int kGroupMembers = 64 / kGroupLanes;
-// Waves per SIMD the group tail runs at. With its members' weights in registers it needs 218
-// VGPRs at C = 2 (H = 64), so two waves share a SIMD and the tail takes over at twice the
-// survivors per CU; at C = 4 it needs 256 + 66 AGPRs, one wave per SIMD. (Reloading the
-// weights every step instead fits two waves at C = 4, 206 VGPRs, but the ES rollout at
-// N = 262,144 and 8 sweeps took 60.6 instead of 50.0 ms: a SIMD holding two long-lived
-// members' waves steps each at part speed to the end of the horizon.)
+// Waves per SIMD the group tail runs at; it takes over at 4 x kTailWaves x kTailMembers
+// survivors per CU. With its members' weights in registers the 16-lane form needed 218 VGPRs
+// at C = 2 (H = 64), so two waves shared a SIMD; at C = 4 it needs 256 VGPRs + 14 AGPRs, one
+// wave per SIMD. (Reloading the weights every step instead fits two waves at C = 4, 206 VGPRs,
+// but the ES rollout at N = 262,144 and 8 sweeps took 60.6 instead of 50.0 ms: a SIMD holding
+// two long-lived members' waves steps each at part speed to the end of the horizon.)
+#ifndef LEGGED_SMALL_TAIL_WAVES
+#define LEGGED_SMALL_TAIL_WAVES 1
+#endif
 template <int C>
-constexpr int kTailWaves = C <= 2 ? 2 : 1;
+constexpr int kTailWaves = C > 2 ? 1 : kTailLanes<C> == 16 ? 2 : LEGGED_SMALL_TAIL_WAVES;
 // Whether chunks between the tail's bound and LEGGED_GROUP_CHUNK_MEMBERS_PER_CU run in the
 // group form. At C <= 2 the tail already takes over at 32 per CU; with 4-lane groups at one
 // wave per SIMD the biped's group chunks between 32 and 64 per CU also pay (biped ES rollout
@@ -1339,8 +1349,8 @@ __global__ __launch_bounds__(64, kTailWaves<C>) void rollout_tail_kernel(Packed 
                                                           float* __restrict__ steps_out, int64_t wide_max) {
   const int64_t count = (int64_t)*src.count;
   if (count > wide_max) return;
-  LEGGED_GROUP_LDS(C, HID, kGroupMembers);
-  rollout_group<C, HID, kGroupLanes, false>(src, src, count, cap, horizon, horizon, iters, alive_bonus, fall, gate,
+  LEGGED_GROUP_LDS(C, HID, kTailMembers<C>);
+  rollout_group<C, HID, kTailLanes<C>, false>(src, src, count, cap, horizon, horizon, iters, alive_bonus, fall, gate,
                                             assist, assist_damping, fitness, steps_out, xs_all, xh_all, xl_all,
                                             xd_all);
 }
@@ -1551,7 +1561,7 @@ struct GroupBounds {
 template <int C>
 inline GroupBounds group_bounds(int64_t p, int cus) {
   GroupBounds b;
-  b.wide_max = (int64_t)LEGGED_TAIL_MEMBERS_PER_CU * kTailWaves<C> * cus;
+  b.wide_max = (int64_t)4 * kTailWaves<C> * kTailMembers<C> * cus;
   const int64_t gm = kGroupChunks<C> ? (int64_t)LEGGED_GROUP_CHUNK_MEMBERS_PER_CU * cus : 0;
   b.group_max = gm > b.wide_max ? gm : b.wide_max;
   // one member group per workgroup: a kernel never holds more than min(p, its bound) members
@@ -1559,7 +1569,7 @@ inline GroupBounds group_bounds(int64_t p, int cus) {
   const int64_t tail_members = p < b.wide_max ? p : b.wide_max;
   constexpr int chunk_members = 64 / kChunkGroupLanes;  // per single-wave workgroup
   b.group_grid = (group_members + chunk_members - 1) / chunk_members;
-  b.tail_grid = (tail_members + kGroupMembers - 1) / kGroupMembers;
+  b.tail_grid = (tail_members + kTailMembers<C> - 1) / kTailMembers<C>;
   return b;
 }
 
