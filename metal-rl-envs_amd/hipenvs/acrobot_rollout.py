@@ -24,7 +24,7 @@ def rollout_steps(state, theta_pop, hidden, horizon):
     horizon = _lib.check_horizon(horizon)
     theta_pop = _lib.check_theta(theta_pop, p, n_params(hidden), state.device)
     steps = torch.empty(p, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_acrobot_es_rollout", _lib.ptr(state), _lib.ptr(theta_pop), p, hidden, horizon,
                   _lib.ptr(steps), _lib.stream_of(state.device))
     return steps
@@ -42,7 +42,7 @@ def rollout_steps_seeded(state, theta, seed, sigma, hidden, horizon):
     theta = _lib.check_theta_vector(theta, d, state.device)
     workspace = torch.empty((p, d), dtype=torch.float32, device=state.device)
     out = torch.empty(p, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_acrobot_es_rollout_seeded", _lib.ptr(state), _lib.ptr(theta), p, _lib.u32(seed),
                   float(sigma), hidden, horizon, _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * 4,
                   _lib.stream_of(state.device))
@@ -59,7 +59,7 @@ def evaluate(state, theta, hidden, steps):
     steps = _lib.check_horizon(steps)
     theta = _lib.check_theta_vector(theta, n_params(hidden), state.device)
     out = torch.empty(n, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_acrobot_evaluate", _lib.ptr(state), _lib.ptr(theta), n, hidden, steps, _lib.ptr(out),
                   _lib.stream_of(state.device))
     return out

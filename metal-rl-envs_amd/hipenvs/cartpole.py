@@ -57,7 +57,7 @@ def reset(n, seed=None, device=None):
         seed = RESET_SEED_BASE + _reset_calls
         _reset_calls += 1
     state = torch.empty((ROWS, n), dtype=torch.float32, device=device)
-    with torch.cuda.device(device):
+    with _lib.on(device):
         _lib.call("hipenvs_cartpole_reset", _lib.ptr(state), n, _lib.u32(seed), _lib.stream_of(device))
     return state
 
@@ -73,7 +73,7 @@ def step(state, action):
     next_state = torch.empty_like(state)
     reward = torch.empty(n, dtype=torch.float32, device=device)
     done = torch.empty(n, dtype=torch.bool, device=device)
-    with torch.cuda.device(device):
+    with _lib.on(device):
         _lib.call("hipenvs_cartpole_step", _lib.ptr(state), _lib.ptr(action), _lib.u32(_calls),
                   _lib.ptr(next_state), _lib.ptr(reward), _lib.ptr(done), n, _lib.stream_of(device))
     return next_state, reward, done
@@ -103,7 +103,7 @@ def step_k(state, k, actions=None):
     if k == 0:
         next_state.copy_(state)
         return next_state, rewards, dones
-    with torch.cuda.device(device):
+    with _lib.on(device):
         _lib.call("hipenvs_cartpole_step_k", _lib.ptr(state), _lib.ptr(actions), _lib.u32(seed), k,
                   _lib.ptr(next_state), _lib.ptr(rewards), _lib.ptr(dones), n, _lib.stream_of(device))
     return next_state, rewards, dones
@@ -116,6 +116,6 @@ def sample_actions(n, seed, m=2, device=None, out=None):
         out = torch.empty(n, dtype=torch.int32, device=device)
     elif out.dtype != torch.int32 or out.shape != (n,) or not out.is_contiguous():
         raise ValueError("out must be a contiguous (n,) int32 tensor")
-    with torch.cuda.device(device):
+    with _lib.on(device):
         _lib.call("hipenvs_sample_actions", _lib.ptr(out), n, int(m), _lib.u32(seed), _lib.stream_of(device))
     return out

@@ -23,7 +23,7 @@ def rollout_steps(state, theta_pop, hidden, horizon):
     horizon = _lib.check_horizon(horizon)
     theta_pop = _lib.check_theta(theta_pop, p, n_params(hidden), state.device)
     fitness = torch.empty(p, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_cartpole_es_rollout", _lib.ptr(state), _lib.ptr(theta_pop), p, hidden, horizon,
                   _lib.ptr(fitness), _lib.stream_of(state.device))
     return fitness
@@ -41,7 +41,7 @@ def rollout_steps_seeded(state, theta, seed, sigma, hidden, horizon):
     theta = _lib.check_theta_vector(theta, d, state.device)
     workspace = torch.empty((p, d), dtype=torch.float32, device=state.device)
     out = torch.empty(p, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_cartpole_es_rollout_seeded", _lib.ptr(state), _lib.ptr(theta), p, _lib.u32(seed),
                   float(sigma), hidden, horizon, _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * 4,
                   _lib.stream_of(state.device))
@@ -58,7 +58,7 @@ def evaluate(state, theta, hidden, steps):
     steps = _lib.check_horizon(steps)
     theta = _lib.check_theta_vector(theta, n_params(hidden), state.device)
     out = torch.empty(n, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_cartpole_evaluate", _lib.ptr(state), _lib.ptr(theta), n, hidden, steps, _lib.ptr(out),
                   _lib.stream_of(state.device))
     return out

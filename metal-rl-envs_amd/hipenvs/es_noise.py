@@ -37,7 +37,7 @@ def perturb(theta, p, seed, sigma, layout="rows"):
     theta = _lib.check_theta_vector(theta, d, theta.device)
     shape = (p, d) if layout == "rows" else (d, p)
     out = torch.empty(shape, dtype=torch.float32, device=theta.device)
-    with torch.cuda.device(theta.device):
+    with _lib.on(theta.device):
         _lib.call("hipenvs_es_perturb", _lib.ptr(theta), d, p, _lib.u32(seed), float(sigma), LAYOUTS[layout],
                   _lib.ptr(out), _lib.stream_of(theta.device))
     return out
@@ -64,7 +64,7 @@ def update_static(theta, ranks, seed, sigma, lr, out):
               and out.device == theta.device and out.is_contiguous())
     if not out_ok:
         raise ValueError(f"out must be a contiguous float32 ({d},) tensor on {theta.device}")
-    with torch.cuda.device(theta.device):
+    with _lib.on(theta.device):
         _lib.call("hipenvs_es_update_static", _lib.ptr(theta), _lib.ptr(ranks), d, p, _lib.u32(seed), float(sigma),
                   float(lr), _lib.ptr(out), _lib.stream_of(theta.device))
     return out
@@ -78,7 +78,7 @@ def update(theta, ranks, seed, sigma, lr):
         raise _lib.HipEnvsError(f"hipenvs_es_update: unsupported population ({p}, {d})")
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=theta.device)
     out = torch.empty_like(theta)
-    with torch.cuda.device(theta.device):
+    with _lib.on(theta.device):
         _lib.call("hipenvs_es_update", _lib.ptr(theta), _lib.ptr(ranks), d, p, _lib.u32(seed), float(sigma),
                   float(lr), _lib.ptr(out), _lib.ptr(workspace), nbytes, _lib.stream_of(theta.device))
     return out

@@ -87,7 +87,7 @@ class Legged:
             seed = RESET_SEED_BASE + self.reset_calls
             self.reset_calls += 1
         state = torch.empty((self.rows, n), dtype=torch.float32, device=device)
-        with torch.cuda.device(device):
+        with _lib.on(device):
             _lib.call("hipenvs_legged_reset", self.c, _lib.ptr(self.stand_on(device)), _lib.ptr(state), n,
                       _lib.u32(seed), _lib.stream_of(device))
         return state
@@ -104,7 +104,7 @@ class Legged:
         next_state = torch.empty_like(state)
         reward = torch.empty(n, dtype=torch.float32, device=device)
         done = torch.empty(n, dtype=torch.bool, device=device)
-        with torch.cuda.device(device):
+        with _lib.on(device):
             _lib.call("hipenvs_legged_step", self.c, self.iters, float(assist or 0.0), _lib.ptr(state),
                       _lib.ptr(action), _lib.u32(self.calls), _lib.ptr(self.stand_on(device)), _lib.ptr(next_state),
                       _lib.ptr(reward), _lib.ptr(done), n, _lib.stream_of(device))
@@ -119,7 +119,7 @@ class Legged:
         next_state = torch.empty((self.rows, n), dtype=torch.float64, device=device)
         reward = torch.empty(n, dtype=torch.float32, device=device)
         done = torch.empty(n, dtype=torch.bool, device=device)
-        with torch.cuda.device(device):
+        with _lib.on(device):
             _lib.call("hipenvs_legged_step_reference", self.c, self.iters, float(assist or 0.0), _lib.ptr(state),
                       is_f64, _lib.ptr(action), _lib.u32(self.calls), _lib.ptr(self.stand_on(device)),
                       _lib.ptr(next_state), _lib.ptr(reward), _lib.ptr(done), n, _lib.stream_of(device))

@@ -73,7 +73,7 @@ def rollout(state, theta_pop, hidden, horizon, c, alive_bonus=1.0, fall_penalty=
     steps = torch.empty(p, dtype=torch.float32, device=state.device)
     args = (float(alive_bonus), float(fall_penalty), float(height_gate), float(assist), _lib.ptr(fitness),
             _lib.ptr(steps))
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         if schedule == "chunked":
             nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=state.device)
@@ -108,7 +108,7 @@ def rollout_seeded(state, theta, seed, sigma, hidden, horizon, c, alive_bonus=1.
     steps = torch.empty(p, dtype=torch.float32, device=state.device)
     nbytes = _lib.lib().hipenvs_legged_es_rollout_workspace_bytes(c, hidden, p)
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_legged_es_rollout_seeded", c, hidden, int(iters), int(chunk_steps), _lib.ptr(state),
                   _lib.ptr(theta), p, _lib.u32(seed), float(sigma), horizon, float(alive_bonus),
                   float(fall_penalty), float(height_gate), float(assist), _lib.ptr(fitness), _lib.ptr(steps),
@@ -131,7 +131,7 @@ def evaluate(state, theta, hidden, steps, c, iters=8, eval_bonus=0.0):
     steps = _lib.check_horizon(steps)
     theta = _lib.check_theta_vector(theta, n_params(hidden, c), state.device)
     out = torch.empty(n, dtype=torch.float32, device=state.device)
-    with torch.cuda.device(state.device):
+    with _lib.on(state.device):
         _lib.call("hipenvs_legged_evaluate", c, hidden, int(iters), _lib.ptr(state), _lib.ptr(theta), n, steps,
                   float(eval_bonus), _lib.ptr(out), _lib.stream_of(state.device))
     return out

@@ -49,7 +49,7 @@ class Pendulum:
             seed = RESET_SEED_BASE + self.reset_calls
             self.reset_calls += 1
         state = torch.empty((2 * self.k, n), dtype=torch.float32, device=device)
-        with torch.cuda.device(device):
+        with _lib.on(device):
             _lib.call("hipenvs_pendulum_aba_reset", self.k, int(bool(zero_velocity)), _lib.ptr(state), n,
                       _lib.u32(seed), _lib.stream_of(device))
         return state
@@ -75,7 +75,7 @@ class Pendulum:
         next_state = torch.empty_like(state)
         reward = torch.empty(n, dtype=torch.float32, device=device)
         done = torch.empty(n, dtype=torch.bool, device=device)
-        with torch.cuda.device(device):
+        with _lib.on(device):
             _lib.call(entry, self.k, _lib.ptr(state), _lib.ptr(extra), _lib.u32(self.calls), _lib.ptr(next_state),
                       _lib.ptr(reward), _lib.ptr(done), n, _lib.stream_of(device))
         return next_state, reward, done
@@ -85,7 +85,7 @@ class Pendulum:
         n = _lib.check_state(state, 2 * self.k)
         torque = _lib.as_f32_vector(torque, n, state.device, "torque")
         acc = torch.empty((self.k, n), dtype=torch.float32, device=state.device)
-        with torch.cuda.device(state.device):
+        with _lib.on(state.device):
             _lib.call("hipenvs_pendulum_aba_accelerations", self.k, _lib.ptr(state), _lib.ptr(torque), _lib.ptr(acc),
                       n, _lib.stream_of(state.device))
         return acc
