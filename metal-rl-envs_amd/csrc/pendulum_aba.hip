@@ -152,13 +152,17 @@ __device__ __forceinline__ void accelerations_with(const float* th, const float*
 
 // accelerations_with through the pivots' shared float64 reciprocals (DivRecip: the IEEE
 // quotient unless it is subnormal); a lane on which a quotient came out subnormal
-// evaluates again with IEEE division, so the results are IEEE's bit for bit. Semi-implicit
-// Euler at N = 65,536: K = 16 11.98 -> 11.35 us per step; K = 4, at the launch floor, 3.75 ->
-// 3.82 us. Past K = 16 the second copy of the evaluation costs scratch (the K = 32 Euler
-// step spilled 184 B/lane). So K = 5..16 divide this way, the others with IEEE division.
+// evaluates again with IEEE division, so the results are IEEE's bit for bit. At N = 65,536:
+// the Euler step at K = 16 11.98 -> 11.35 us, at K = 4 3.23 -> 3.14 us; the RK4 step at
+// K = 4 6.77 -> 6.46 us. Past K = 16 the second copy of the evaluation costs scratch (the
+// K = 32 Euler step spilled 184 B/lane). So K = 2..16 divide this way, the others with IEEE
+// division (one link has one quotient to share its reciprocal with).
+#ifndef ABA_RECIP_MIN_K
+#define ABA_RECIP_MIN_K 2
+#endif
 template <int K, int U = K>
 __device__ __forceinline__ void accelerations(const float* th, const float* om, float torque, float* acc) {
-  if constexpr (K > 4 && K <= 16) {
+  if constexpr (K >= ABA_RECIP_MIN_K && K <= 16) {
     DivRecip fast;
     accelerations_with<K, U>(th, om, torque, acc, fast);
     if (fast.saw_subnormal()) {
