@@ -65,7 +65,9 @@ sample of about `--cpu-seconds` seconds on this host.
 * `es_evaluate`: the learner's greedy evaluation of the mean policy (es.py:308-322,
   2,048 envs x 500 steps): the fused one-launch kernel against the reference's
   loop (torch mean policy + one env-step launch per iteration); wall time, median
-  of repeats, and both scores.
+  of repeats, and both scores. CartPole, Acrobot and legged4 from theta = 0.1 N(0, 1);
+  legged4_standing from a policy whose bodies stand for all 500 steps, as a trained
+  one's do;
 
 Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--repeats 3] [--sweep] [--skip-cpu]
                       [--only cartpole|legged|aba|steps]
@@ -809,11 +811,19 @@ def bench_es_evaluate(dev, repeats):
     from hipenvs import es
 
     out = {}
-    for name, hidden in (("cartpole", 32), ("acrobot", 32), ("legged4", 64)):
-        task = es.TASKS[name]
+    # legged4_standing: small weights and head biases that pick each leg's zero-torque action,
+    # a policy that stands for the whole evaluation as a trained one does (long episodes)
+    for name, hidden in (("cartpole", 32), ("acrobot", 32), ("legged4", 64), ("legged4_standing", 64)):
+        task = es.TASKS[name.replace("_standing", "")]
         g = torch.Generator(device=dev)
         g.manual_seed(1)
         theta = torch.randn(es.n_params(hidden, task), generator=g, device=dev) * 0.1
+        if name.endswith("_standing"):
+            c = 4
+            obs, outs = 5 + 2 * c, 3 * c
+            theta = theta * 0.2
+            b2 = obs * hidden + hidden + hidden * outs
+            theta[b2 + 1:b2 + outs:3] = 1.0
         rec = {"n": 2048, "steps": 500, "hidden": hidden}
         for label, fn in (("fused", lambda: es.evaluate_theta(task, theta, hidden, device=dev)),
                           ("loop", lambda: es.evaluate(task, es.mean_policy(theta, hidden, task), device=dev))):

@@ -1020,9 +1020,10 @@ struct ResidentPolicy {
   static_assert(OUT <= G, "one head per lane");
   float w1[U][OBS], b1[U], w2[HID], b2;
 
+  // from a member's weights in a 64-member tile (UnitRows, stride 64), or with R = FlatRows
+  // and kStride 1 from one policy in es.unflatten's layout
+  template <class R = UnitRows<OBS, HID, OUT>, int64_t kStride = 64>
   __device__ __forceinline__ void load(const float* __restrict__ w, int g) {
-    using R = UnitRows<OBS, HID, OUT>;
-    constexpr int64_t kStride = 64;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = g + G * u < HID ? g + G * u : 0;  // lanes past HID hold unit 0, unused
@@ -1353,6 +1354,52 @@ __global__ __launch_bounds__(64, kTailWaves<C>) void rollout_tail_kernel(Packed 
   rollout_group<C, HID, kTailLanes<C>, false>(src, src, count, cap, horizon, horizon, iters, alive_bonus, fall, gate,
                                             assist, assist_damping, fitness, steps_out, xs_all, xh_all, xl_all,
                                             xd_all);
+}
+
+// The greedy evaluation (evaluate_kernel) with a group of kTailLanes<C> lanes per env, for
+// batches of at most one wave per SIMD: one env per lane leaves most SIMDs idle there, and a
+// policy that stands steps every env to the end at one lane's latency. The shared policy's
+// weights are loaded into the group's registers once; the step is the group tail's (same
+// bits as the one-lane kernel).
+template <int C, int HID>
+__global__ __launch_bounds__(64, kTailWaves<C>) void evaluate_group_kernel(const float* __restrict__ state,
+                                                                          const float* __restrict__ theta,
+                                                                          int64_t n, int32_t steps, int iters,
+                                                                          float eval_bonus,
+                                                                          float* __restrict__ fitness) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C, G = kTailLanes<C>, M = kTailMembers<C>;
+  LEGGED_GROUP_LDS(C, HID, M);
+  const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
+  float* xs = xs_all + mloc * (2 * C + 1) * 8;
+  float* xd = xd_all + mloc * kBlockFloats<C>;
+  float* xh = xh_all + mloc * HID;
+  float* xl = xl_all + mloc * 16;
+  const int64_t e = (int64_t)blockIdx.x * M + mloc;
+  bool live = e < n && steps > 0;
+  const int64_t slot = e < n ? e : n - 1;  // a group past n steps env n - 1, unused
+  float q[N], v[N], tq[C];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = state[i * n + slot];
+    v[i] = state[(N + i) * n + slot];
+  }
+  ResidentPolicy<C, HID, G> policy;
+  policy.template load<FlatRows<OBS, HID, OUT>, 1>(theta, g);
+  float total = 0.0f;
+  // every lane steps while any env of the wave is live, so the barriers stay uniform
+  for (int32_t t = 0; t < steps && __any(live); ++t) {
+    policy.policy(q, v, tq, xh, xl, g);
+#pragma unroll 1
+    for (int sub = 0; sub < SUBSTEPS; ++sub)
+      substep_exact_group<C, G>(q, v, tq, iters, 0.0f, 0.0f, xs, g, live, xd);
+    if (live) {
+      if (fallen<C>(q))
+        live = false;
+      else
+        total = total + (((v[0] + 1.0f) - 1.0f) + eval_bonus);
+    }
+  }
+  if (g == 0 && e < n) fitness[e] = total;
 }
 
 // The group form for one chunk, G lanes per member, when the set holds more than lo and at
@@ -1710,10 +1757,30 @@ int dispatch_chunked_seeded(int32_t hidden, const float* state, const float* the
   }
 }
 
+#ifndef LEGGED_EVALUATE_GROUP
+#define LEGGED_EVALUATE_GROUP 1
+#endif
 template <int C>
 int launch_evaluate(int32_t hidden, const float* state, const float* theta, int64_t n, int32_t steps, int iters,
                     float eval_bonus, float* fitness, hipStream_t s) {
   const dim3 grid(grid_for(n, 64)), block(64);
+  int cus = 0;
+  const int query = device_cus(&cus);
+  if (query != HIPENVS_OK) return query;
+  // a batch that the group form holds at one wave per SIMD takes it (one lane per env would
+  // leave most SIMDs idle and step each env at one lane's latency)
+  if (LEGGED_EVALUATE_GROUP && n <= (int64_t)4 * kTailWaves<C> * kTailMembers<C> * cus) {
+    const dim3 ggrid((unsigned)((n + kTailMembers<C> - 1) / kTailMembers<C>));
+    switch (hidden) {
+      case 4: hipLaunchKernelGGL((evaluate_group_kernel<C, 4>), ggrid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+      case 8: hipLaunchKernelGGL((evaluate_group_kernel<C, 8>), ggrid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+      case 16: hipLaunchKernelGGL((evaluate_group_kernel<C, 16>), ggrid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+      case 32: hipLaunchKernelGGL((evaluate_group_kernel<C, 32>), ggrid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+      case 64: hipLaunchKernelGGL((evaluate_group_kernel<C, 64>), ggrid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
+      default: return HIPENVS_E_UNSUPPORTED;
+    }
+    return launch_status();
+  }
   switch (hidden) {
     case 4: hipLaunchKernelGGL((evaluate_kernel<C, 4>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;
     case 8: hipLaunchKernelGGL((evaluate_kernel<C, 8>), grid, block, 0, s, state, theta, n, steps, iters, eval_bonus, fitness); break;

@@ -55,6 +55,48 @@ def test_legged_evaluate_matches_oracle(dev, c, hidden):
     assert np.any(expect != 0)
 
 
+def standing_theta(hidden, c, scale=0.02, seed=5):
+    """Small random weights and head biases that favour each leg's middle (zero-torque) action:
+    a policy under which the bodies stand for the whole evaluation, as a trained one does."""
+    from hipenvs import legged_rollout
+
+    obs, out = 5 + 2 * c, 3 * c
+    theta = shared_theta(legged_rollout.n_params(hidden, c), seed, scale=scale)
+    b2 = obs * hidden + hidden + hidden * out
+    for leg in range(c):
+        theta[b2 + 3 * leg + 1] = 1.0
+    return theta
+
+
+@pytest.mark.parametrize("c,hidden", [(2, 64), (3, 16), (4, 64)])
+def test_legged_evaluate_standing_policy(dev, c, hidden):
+    """Long episodes in the group form (batches of at most one wave per SIMD): most envs stand
+    for every step, and the per-env sums equal the oracle's bit for bit."""
+    from hipenvs import legged, legged_rollout
+
+    n, steps = 300, 150
+    theta = standing_theta(hidden, c)
+    state = legged.Legged(c).reset(n, seed=31, device=dev)
+    got = legged_rollout.evaluate(state, torch.from_numpy(theta).to(dev), hidden, steps, c, eval_bonus=10.0)
+    expect = olg.evaluate_fused(to_np(state), theta, hidden, steps, c, eval_bonus=10.0)
+    np.testing.assert_array_equal(to_np(got), expect)
+    assert np.mean(expect > 10.0 * (steps - 1)) > 0.5  # most envs stood to the end (10 per step)
+
+
+def test_legged_evaluate_one_lane_form(dev):
+    """A batch past the group form's bound (16 envs per CU at C = 4) runs one env per lane:
+    the same sums as the oracle."""
+    from hipenvs import legged, legged_rollout
+
+    c, hidden, steps = 4, 16, 24
+    n = 16 * torch.cuda.get_device_properties(dev).multi_processor_count + 37
+    theta = standing_theta(hidden, c, scale=0.2, seed=6)
+    state = legged.Legged(c).reset(n, seed=32, device=dev)
+    got = legged_rollout.evaluate(state, torch.from_numpy(theta).to(dev), hidden, steps, c)
+    expect = olg.evaluate_fused(to_np(state), theta, hidden, steps, c)
+    np.testing.assert_array_equal(to_np(got), expect)
+
+
 @pytest.mark.parametrize("task_name", ["cartpole", "acrobot", "legged2"])
 def test_learner_score_matches_torch_loop(dev, task_name):
     """es.evaluate_theta (one fused launch) against es.evaluate with the torch mean policy and
