@@ -146,8 +146,8 @@ def test_bad_populations_are_rejected(dev):
 def test_config4_full_size_schedules_agree(dev, c, iters):
     """At the benchmark's full shape (N = 262,144, H = 64, horizon 1,000, sigma 0.03 around
     0.1 N(0, 1)) for the quadruped and the biped at S = 4, 8, 16: the seeded rollout, the
-    chunked rollout of the perturbed columns and the one-member-per-lane rollout of the
-    perturbed rows agree member for member."""
+    chunked rollout of the perturbed columns, the chunked rollout of the perturbed rows (the
+    drop-in call) and the one-member-per-lane rollout of the rows agree member for member."""
     from hipenvs import es_noise, legged, legged_rollout
 
     p, hidden = 262_144, 64
@@ -160,6 +160,9 @@ def test_config4_full_size_schedules_agree(dev, c, iters):
     del cols
     rows = es_noise.perturb(theta, p, 5, 0.03)
     fr, sr = legged_rollout.rollout(state, rows, hidden, 1000, c, schedule="rows", iters=iters)
+    # the drop-in call: the chunked schedule reading the (P, D) rows in its first chunk
+    fd, sd = legged_rollout.rollout(state, rows, hidden, 1000, c, iters=iters)
     assert torch.equal(fs, fc) and torch.equal(ss, sc)
     assert torch.equal(fs, fr) and torch.equal(ss, sr)
+    assert torch.equal(fs, fd) and torch.equal(ss, sd)
     assert sr.max().item() == 1000 or sr.max().item() > 300  # a long tail reaches the group phase
