@@ -57,7 +57,7 @@ def test_acrobot_evaluate_is_minus_steps():
     assert fused.min() < 0
 
 
-@pytest.mark.parametrize("c", [2, 4])
+@pytest.mark.parametrize("c", [1, 2, 3, 4])
 def test_legged_evaluate_is_forward_distance(c):
     hidden, n, steps = 8, 48, 60
     theta = shared_theta(olg_n_params(hidden, c), 3 + c, scale=0.3)
