@@ -38,7 +38,7 @@ def test_config2_fitness_under_the_reference_trig(name):
     assert same >= (1.0 if name == "cartpole" else 0.99), same  # measured
 
 
-@pytest.mark.parametrize("c,measured_close", [(2, 1.0), (4, 0.98)])
+@pytest.mark.parametrize("c,measured_close", [(1, 0.99), (2, 1.0), (4, 0.98)])
 def test_legged_fused_float32_against_the_reference_loop(c, measured_close):
     """The fused float32 legged rollout (the HIP kernels' arithmetic: float32 physics,
     deterministic trig, bias-first policy sums) against the reference's numpy loop: es.py's
@@ -67,3 +67,40 @@ def test_legged_fused_float32_against_the_reference_loop(c, measured_close):
     close = np.abs(fit_k - fit_l) <= 1e-3 * np.maximum(np.abs(fit_l), 1.0) + 1e-2
     assert close.mean() > 0.95 and (steps_k == steps_l).mean() > 0.95   # the reference's gate
     assert close.mean() >= measured_close and (steps_k == steps_l).mean() >= measured_close
+
+
+def test_legged3_fused_float32_against_the_reference_loop():
+    """The same comparison at C = 3, a leg count the reference's tasks do not use. The float32
+    trajectories leave numpy's float64-promoted ones chaotically as the horizon grows: equal
+    episode lengths for every member to step 25, 98.4 % at 50, 96.5 % at 100 and 91.4 % at 200
+    (fitness within the tolerance: 98.4, 94.9, 88.7, 84.8 %), so the reference's 95 % gate
+    holds to about 100 steps here; each step's distance is bounded by the C = 3 golden
+    fixtures. The float32 step loop itself (es.loop_fitness over the oracle's float32 step
+    and policy) takes exactly the fused rollout's steps: the composition is exact."""
+    c, p, hidden, horizon = 3, 256, 64, 200
+    r = np.random.default_rng(c)
+    d = es.n_params(hidden, 5 + 2 * c, 3 * c)
+    theta0 = (r.standard_normal(d) * 0.1).astype(np.float32)
+    half = r.standard_normal((p // 2, d)).astype(np.float32)
+    pop = (theta0[None, :] + np.float32(0.03) * np.concatenate([half, -half])).astype(np.float32)
+    state = olg.Legged(c).reset(p, seed=3)
+    fit_k, steps_k = olg.rollout_fused(state, pop, hidden, horizon, c)
+    w = es.unflatten(pop, hidden, 5 + 2 * c, 3 * c)
+
+    def logits32(st):
+        return olg.policy_logits(st[:3 + c], st[3 + c:], *w, c).T
+
+    _, steps_f = es.loop_fitness(olg.Legged(c, 8, mode="f32").step, logits32, lambda lg: es.legged_action(lg, c),
+                                 state, (), horizon, seed0=1)
+    np.testing.assert_array_equal(steps_f, steps_k)
+    w1, b1, w2, b2 = w
+    body = olg.Legged(c, 8, mode="reference", trig="numpy")
+
+    def logits(st):
+        h = np.tanh(np.einsum("pi,pih->ph", st[1:].T, w1) + b1)
+        return np.einsum("ph,pho->po", h, w2) + b2
+
+    fit_l, steps_l = es.loop_fitness(body.step, logits, lambda lg: es.legged_action(lg, c), state, (), horizon,
+                                     seed0=1)
+    close = np.abs(fit_k - fit_l) <= 1e-3 * np.maximum(np.abs(fit_l), 1.0) + 1e-2
+    assert close.mean() >= 0.84 and (steps_k == steps_l).mean() >= 0.91  # measured
