@@ -393,7 +393,15 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     const int sel = (g == 2) ? 1 : (g == 3) ? 2 : 0;       // det, den_p, den_m
     const uint32_t neg = nrow ? 0x80000000u : 0u;
     const int oA = nrow ? 2 : 0, oB = nrow ? 3 : 1, oQ = nrow ? 1 : 0;  // Ant|Att, Ann|Atn, Atn|Att
+    // Lanes 2 and 3 clamp their cone-edge quotients before the broadcast, as the contact solve
+    // does after it: (den > 0) ? max0(q) : 0, that is 0 where den > 0 fails or q < 0, else q
+    // (-0 and NaN pass, as in max0). Lanes 0 and 1 compare against -inf, which nothing is
+    // below, and pass their stick quotients on unchanged. One clamp on two lanes replaces two
+    // on every lane.
+    const bool edge = (g == 2 || g == 3);
+    const float qlo = edge ? 0.0f : -__builtin_inff();
     float cA[C][C], cB[C][C], w0x[C], qP[C], qQ[C], qd[C], slipc[C];
+    bool qzero[C];
     double qr[C];
 #pragma unroll
     for (int k = 0; k < C; ++k) {
@@ -412,6 +420,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       const float* xc = xd + 4 * C * C + 12 * k;
       qd[k] = xc[sel];
       qr[k] = *reinterpret_cast<const double*>(xc + 4 + 2 * sel);
+      qzero[k] = edge && !(qd[k] > 0.0f);  // lane 2 holds den_p, lane 3 den_m
       slipc[k] = blk[k].Att * MU + blk[k].Atn;
     }
     for (int it = 0; it < iters; ++it) {
@@ -435,19 +444,17 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
           wt = lane_bcast<kGroup, 0>(wx);
           wn = lane_bcast<kGroup, 1>(wx);
         }
-        const ContactBlock& b = blk[k];
         const bool touching = depth[k] >= 0.0f;
         const float target = BAUMGARTE_OVER_H * max0(depth[k]);
         const float tw = target - wn;
-        const float num = (g == 2 || g == 3) ? tw : qP[k] * wt + qQ[k] * tw;
+        const float num = edge ? tw : qP[k] * wt + qQ[k] * tw;
         const float quo = div(num, qd[k], qr[k]);
-        const float ln_stick = lane_bcast<kGroup, 0>(quo);
-        const float lt_stick = lane_bcast<kGroup, 1>(quo);
-        const float q_p = lane_bcast<kGroup, 2>(quo);
-        const float q_m = lane_bcast<kGroup, 3>(quo);
+        const float qc = (qzero[k] || quo < qlo) ? 0.0f : quo;
+        const float ln_stick = lane_bcast<kGroup, 0>(qc);
+        const float lt_stick = lane_bcast<kGroup, 1>(qc);
+        const float ln_p = lane_bcast<kGroup, 2>(qc);
+        const float ln_m = lane_bcast<kGroup, 3>(qc);
         const bool sticks = fabsf(lt_stick) <= MU * ln_stick;
-        const float ln_p = (b.den_p > 0.0f) ? max0(q_p) : 0.0f;
-        const float ln_m = (b.den_m > 0.0f) ? max0(q_m) : 0.0f;
         const float slip_p = wt + slipc[k] * ln_p;
         const float sgn = (slip_p <= 0.0f) ? 1.0f : -1.0f;
         const float ln_slide = (slip_p <= 0.0f) ? ln_p : ln_m;
