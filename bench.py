@@ -70,7 +70,7 @@ sample of about `--cpu-seconds` seconds on this host.
   one's do;
 
 Usage: python bench.py [--gpus 1] [--steps 1000] [--warmup 16] [--repeats 3] [--sweep] [--skip-cpu]
-                      [--only cartpole|legged|aba|steps]
+                      [--only cartpole|legged|aba|steps|generation]
 """
 
 import argparse
@@ -131,10 +131,10 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--legged-cpu-seconds", type=float, default=12.0)
     p.add_argument("--skip-cpu", action="store_true")
-    p.add_argument("--only", choices=["cartpole", "legged", "aba", "steps"], default=None,
+    p.add_argument("--only", choices=["cartpole", "legged", "aba", "steps", "generation"], default=None,
                    help="run one block: the CartPole headline, the legged rollouts (then the line's value is the "
-                        "legged4 S = 8 rollout), the ABA Euler step, or the ABA Euler step and the other step "
-                        "bodies (the last two for counter collection; no line)")
+                        "legged4 S = 8 rollout), the ABA Euler step, the ABA Euler step and the other step "
+                        "bodies, or the whole ES generations (the last three for counter collection; no line)")
     p.add_argument("--legged-n", type=int, default=262144)
     p.add_argument("--legged-horizon", type=int, default=1000)
     p.add_argument("--sweep", action="store_true", help="also run the CartPole N = 2^0..2^24 sweep")
@@ -1168,6 +1168,10 @@ def main():
         if args.only == "steps":
             extra["step_bodies"] = bench_step_bodies(dev)
             extra["legged_step_sweeps"] = bench_legged_step_sweep(dev)
+        print(json.dumps(extra), flush=True)
+        return
+    if args.only == "generation":
+        extra["es_generation"] = bench_es_generation(dev, args.repeats, args.legged_n, args.legged_horizon)
         print(json.dumps(extra), flush=True)
         return
     if args.only is None:

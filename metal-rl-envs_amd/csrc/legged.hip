@@ -1478,12 +1478,13 @@ __global__ __launch_bounds__(64, kFirst ? LEGGED_FIRST_CHUNK_MIN_WAVES : LEGGED_
       if constexpr (kRows) {
         policy_torques_rows<C, HID>(MemberRow(stheta, p * (int64_t)D, i, D), q, v, tq);
       } else if constexpr (kFirst) {
-        // the column base passes through an empty asm statement every step, so the loads
+        // an offset of zero passes through an empty asm statement every step, so the loads
         // (the same addresses each step) stay in the loop: at H = 4 the compiler had
-        // hoisted all 120 weights into registers and spilled 60 B/lane
-        const float* wk = w;
-        if constexpr (LEGGED_FIRST_CHUNK_OPAQUE_COLUMNS != 0) asm volatile("" : "+v"(wk));
-        policy_torques<C, HID>(wk, src_stride, q, v, tq);
+        // hoisted all 120 weights into registers and spilled 60 B/lane. The column pointer
+        // keeps its base, so they stay global loads (an opaque pointer made them flat loads).
+        uint32_t off = 0;
+        if constexpr (LEGGED_FIRST_CHUNK_OPAQUE_COLUMNS != 0) asm volatile("" : "+v"(off));
+        policy_torques<C, HID>(w + off, src_stride, q, v, tq);
       } else {
         policy_torques<C, HID, UnitRows, kTile>(w, kTile, q, v, tq);
       }
@@ -1606,6 +1607,213 @@ __global__ __launch_bounds__(64) void seed_set_kernel(const float* __restrict__ 
   }
 }
 
+// ---- the seeded rollout's first chunk over antithetic pairs ----
+// Members m and m + p/2 of a seeded population share one noise row e = sigma * eps_m (their
+// weights are theta + e and theta + (-e)). The first chunk reads that row once for both. The
+// rows lie in tiles of kPairTile pairs (UnitRows order, row r of pair q at
+// ((q / kPairTile) * D + r) * kPairTile + q % kPairTile), a wave runs one tile, and lanes l
+// and l + 32 hold members q and q + p/2, so their loads of a row are the same 128 bytes:
+// half of the weight bytes a wave of 64 members reads from a full population. A lane forms
+// each weight as fmaf(s, e, theta_k) with s = +1 or -1. The product is exact, so this is
+// theta_k + e or theta_k + (-e) rounded once, the bits seed_set_kernel stores. theta is read
+// with scalar loads, one copy for the wave.
+constexpr int kPairTile = 32;
+
+// policy_torques of one pair member: weight k is fmaf(sgn, e[row(k) * kPairTile], t0[k]) with
+// e the lane's column of its pair tile and t0 the flat theta. The same batches, order of
+// operations and torques as policy_torques.
+template <int C, int HID>
+__device__ __forceinline__ void policy_torques_pairs(const float* __restrict__ e, const float* __restrict__ t0,
+                                                     float sgn, const float (&q)[3 + C], const float (&v)[3 + C],
+                                                     float (&tq)[C]) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  using F = FlatRows<OBS, HID, OUT>;
+  using R = UnitRows<OBS, HID, OUT>;
+  constexpr int64_t kS = kPairTile;
+  float obs[OBS];
+#pragma unroll
+  for (int k = 1; k < N; ++k) obs[k - 1] = q[k];
+#pragma unroll
+  for (int k = 0; k < N; ++k) obs[N - 1 + k] = v[k];
+  float logit[OUT];
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) logit[o] = __builtin_fmaf(sgn, e[R::b2(o) * kS], t0[F::b2(o)]);
+  constexpr int kWant = C <= 2 ? 4 : 2;
+  constexpr int kBatch = kWant <= HID ? kWant : HID;
+  static_assert(HID % kBatch == 0, "whole batches of hidden units");
+#pragma unroll 2
+  for (int j0 = 0; j0 < HID; j0 += kBatch) {
+    float eb[kBatch][1 + OBS + OUT], tb[kBatch][1 + OBS + OUT];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u;
+      eb[u][0] = e[R::b1(j) * kS];
+      tb[u][0] = t0[F::b1(j)];
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) {
+        eb[u][1 + k] = e[R::w1(k, j) * kS];
+        tb[u][1 + k] = t0[F::w1(k, j)];
+      }
+#pragma unroll
+      for (int o = 0; o < OUT; ++o) {
+        eb[u][1 + OBS + o] = e[R::w2(j, o) * kS];
+        tb[u][1 + OBS + o] = t0[F::w2(j, o)];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      float s = __builtin_fmaf(sgn, eb[u][0], tb[u][0]);
+#pragma unroll
+      for (int k = 0; k < OBS; ++k) s = s + obs[k] * __builtin_fmaf(sgn, eb[u][1 + k], tb[u][1 + k]);
+      const float hj = det_tanh(s);
+#pragma unroll
+      for (int o = 0; o < OUT; ++o)
+        logit[o] = logit[o] + hj * __builtin_fmaf(sgn, eb[u][1 + OBS + o], tb[u][1 + OBS + o]);
+    }
+  }
+#pragma unroll
+  for (int leg = 0; leg < C; ++leg) {
+    float torque = -1.0f, best = logit[3 * leg];
+    if (logit[3 * leg + 1] > best) { torque = 0.0f; best = logit[3 * leg + 1]; }
+    if (logit[3 * leg + 2] > best) { torque = 1.0f; }
+    tq[leg] = torque * TORQUE;
+  }
+}
+
+// A pair member's weights into a UnitRows tile (row stride dst_stride), formed as in
+// policy_torques_pairs, hidden unit j's 1 + OBS + OUT rows at a time.
+template <int OBS, int HID, int OUT>
+__device__ __forceinline__ void copy_pair_to_units(float* __restrict__ dst, int64_t dst_stride,
+                                                   const float* __restrict__ e, const float* __restrict__ t0,
+                                                   float sgn) {
+  using F = FlatRows<OBS, HID, OUT>;
+  using T = UnitRows<OBS, HID, OUT>;
+  constexpr int kUnit = T::kUnit;
+  constexpr int64_t kS = kPairTile;
+#pragma unroll 2
+  for (int j = 0; j < HID; ++j) {
+    float b[kUnit];
+    b[0] = __builtin_fmaf(sgn, e[T::b1(j) * kS], t0[F::b1(j)]);
+#pragma unroll
+    for (int k = 0; k < OBS; ++k) b[1 + k] = __builtin_fmaf(sgn, e[T::w1(k, j) * kS], t0[F::w1(k, j)]);
+#pragma unroll
+    for (int o = 0; o < OUT; ++o) b[1 + OBS + o] = __builtin_fmaf(sgn, e[T::w2(j, o) * kS], t0[F::w2(j, o)]);
+#pragma unroll
+    for (int r = 0; r < kUnit; ++r) dst[(T::b1(j) + r) * dst_stride] = b[r];
+  }
+  float b2[OUT];
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) b2[o] = __builtin_fmaf(sgn, e[T::b2(o) * kS], t0[F::b2(o)]);
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) dst[T::b2(o) * dst_stride] = b2[o];
+}
+
+// The pair tiles: e = sigma * eps_q for pair q < p/2 (es_noise.h generates eps), one thread
+// per pair.
+template <int C, int HID>
+__global__ __launch_bounds__(64) void seed_pairs_kernel(int64_t p, uint32_t seed, float sigma,
+                                                        float* __restrict__ tiles) {
+  constexpr int OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  const int64_t half = p / 2;
+  const int64_t m = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (m >= half) return;
+  float* e = tiles + (m / kPairTile) * (int64_t)D * kPairTile + (m % kPairTile);
+  const uint32_t key = esn::member_key(seed, (uint32_t)m);
+  for (int j = 0; j < (D + 1) / 2; ++j) {
+    float z0, z1;
+    esn::gauss_pair(key, (uint32_t)j, z0, z1);
+    const int k = 2 * j;
+    e[unit_row_of_flat<OBS, HID, OUT>(k) * kPairTile] = sigma * z0;
+    if (k + 1 < D) e[unit_row_of_flat<OBS, HID, OUT>(k + 1) * kPairTile] = sigma * z1;
+  }
+}
+
+// The seeded rollout's first chunk: wave t runs the pairs of tile t (members q and q + p/2 of
+// each) for chunk_steps steps from the caller's (2N, p) state rows and appends the survivors,
+// their weights formed, to dst. Otherwise as rollout_chunk_kernel's first chunk.
+template <int C, int HID>
+__global__ __launch_bounds__(64, LEGGED_FIRST_CHUNK_MIN_WAVES) void rollout_pairs_first_kernel(
+    const float* __restrict__ state0, const float* __restrict__ theta, const float* __restrict__ tiles, int64_t p,
+    Packed dst, int64_t cap, int32_t chunk_steps, int32_t horizon, int iters, float alive_bonus, float fall,
+    float gate, float assist, float assist_damping, float* __restrict__ fitness, float* __restrict__ steps_out) {
+  constexpr int N = 3 + C, OBS = 5 + 2 * C, OUT = 3 * C;
+  constexpr int D = OBS * HID + HID + HID * OUT + OUT;
+  constexpr bool kStage = LEGGED_CHUNK_STAGE != 0;
+  __shared__ float stage_lds[kStage ? 2 * C * N * 64 : 1];
+  static_assert(2 * kPairTile == 64, "a wave holds both members of its tile's pairs");
+  const unsigned lane = threadIdx.x;
+  const int64_t half = p / 2;
+  const int64_t pair = (int64_t)blockIdx.x * kPairTile + (lane % kPairTile);
+  bool live = pair < half;
+  const bool minus = lane >= (unsigned)kPairTile;
+  const float sgn = minus ? -1.0f : 1.0f;
+  const int64_t i = minus ? half + pair : pair;
+  float q[N], v[N], tq[C];
+  float total = 0.0f, taken = 0.0f;
+  int32_t t = 0;
+  if (live) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      q[r] = state0[r * p + i];
+      v[r] = state0[(N + r) * p + i];
+    }
+  }
+  const float* e = tiles + (int64_t)blockIdx.x * D * kPairTile + (lane % kPairTile);
+  for (int32_t k = 0; k < chunk_steps; ++k) {
+    if (!__any(live)) break;
+    if (!live) continue;
+    // offsets of zero pass through empty asm statements every step, so the loads (the same
+    // addresses each step) stay in the loop instead of being hoisted into registers; the
+    // pointers keep their bases, so the noise loads stay global loads and theta's scalar
+    uint32_t eoff = 0, toff = 0;
+    asm volatile("" : "+v"(eoff));
+    asm volatile("" : "+s"(toff));
+    policy_torques_pairs<C, HID>(e + eoff, theta + toff, sgn, q, v, tq);
+#pragma unroll 1
+    for (int sub = 0; sub < SUBSTEPS; ++sub)
+      substep_exact<C, false, kStage>(q, v, tq, iters, assist, assist_damping, stage_lds + lane);
+    ++t;
+    bool finished;
+    if (fallen<C>(q)) {
+      taken += 1.0f;
+      total = total - fall;
+      finished = true;
+    } else {
+      total = total + (((q[1] >= gate) ? v[0] : 0.0f) + alive_bonus);
+      taken += 1.0f;
+      finished = t >= horizon;
+    }
+    if (finished) {
+      fitness[i] = total;
+      steps_out[i] = taken;
+      live = false;
+    }
+  }
+  const unsigned long long m = __ballot(live);
+  if (m) {
+    const int leader = __ffsll((long long)m) - 1;
+    unsigned int slot0 = 0;
+    if ((int)lane == leader) slot0 = atomicAdd(dst.count, (unsigned int)__popcll(m));
+    slot0 = __shfl(slot0, leader);
+    if (live) {
+      const int64_t slot = (int64_t)slot0 + __popcll(m & ((1ull << lane) - 1ull));
+#pragma unroll
+      for (int r = 0; r < N; ++r) {
+        dst.state[r * cap + slot] = q[r];
+        dst.state[(N + r) * cap + slot] = v[r];
+      }
+      dst.acc[slot] = total;
+      dst.acc[cap + slot] = taken;
+      dst.meta[slot] = (int32_t)i;
+      dst.meta[cap + slot] = t;
+      float* wd = dst.theta + (slot / kTile) * (int64_t)D * kTile + (slot % kTile);
+      copy_pair_to_units<OBS, HID, OUT>(wd, kTile, e, theta, sgn);
+    }
+  }
+}
+
 // Member counts at which the schedule changes form: one member per lane above group_max,
 // the group chunk kernel above wide_max, the group tail at or below wide_max.
 struct GroupBounds {
@@ -1708,9 +1916,14 @@ int launch_chunked(const float* state, const float* theta0, int64_t p, int32_t h
   return status;
 }
 
-// The seeded rollout: seed_set_kernel writes set 0 (every member, weights generated in
-// place), then every chunk runs in the compacted form, with the group tail after each.
-// Members run the same arithmetic as in launch_chunked on theta + sigma * [eps; -eps].
+// The seeded rollout. Above the group tail's bound, seed_pairs_kernel writes the pair tiles and
+// rollout_pairs_first_kernel runs the first chunk from them; at or below it, seed_set_kernel
+// writes set 0 (every member, weights formed in place) and the tail takes it from step 0.
+// The later chunks run in the compacted form, with the group tail after each. Members run the
+// same arithmetic as in launch_chunked on theta + sigma * [eps; -eps].
+#ifndef LEGGED_SEEDED_PAIRS
+#define LEGGED_SEEDED_PAIRS 1
+#endif
 template <int C, int HID>
 int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uint32_t seed, float sigma,
                           int32_t horizon, int iters, int32_t chunk_steps, float alive, float fall, float gate,
@@ -1742,13 +1955,30 @@ int launch_chunked_seeded(const float* state, const float* theta, int64_t p, uin
   const int64_t grid = resident < needed ? resident : needed;
   const GroupBounds gb = group_bounds<C>(p, cus);
   const float af = (float)assist, ad = (float)(0.1 * assist);
-  hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, (uint32_t)p);
-  hipLaunchKernelGGL((seed_set_kernel<C, HID>), dim3((unsigned)((p / 2 + 63) / 64)), dim3(64), 0, s, state, theta, p,
-                     seed, sigma, set[0], cap);
-  int status = launch_status();
-  int cur = 0;
+  int status, cur;
+  int64_t done = 0;
   int32_t len = first_chunk_steps<C>(chunk_steps);
-  for (int64_t done = 0; status == HIPENVS_OK && done < horizon; done += len, len = chunk_steps) {
+  if (LEGGED_SEEDED_PAIRS && p > gb.wide_max) {
+    // the pair tiles (half of set 0's weight space) feed the first chunk, whose survivors go
+    // to set 1
+    const int64_t tiles = (p / 2 + kPairTile - 1) / kPairTile;
+    hipLaunchKernelGGL((seed_pairs_kernel<C, HID>), dim3((unsigned)((p / 2 + 63) / 64)), dim3(64), 0, s, p, seed,
+                       sigma, set[0].theta);
+    hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[1].count, 0u);
+    hipLaunchKernelGGL((rollout_pairs_first_kernel<C, HID>), dim3((unsigned)tiles), dim3(64), 0, s, state, theta,
+                       set[0].theta, p, set[1], cap, len, horizon, iters, alive, fall, gate, af, ad, fitness, steps);
+    status = launch_status();
+    cur = 1;
+    done = len;
+    len = chunk_steps;
+  } else {
+    hipLaunchKernelGGL(set_count_kernel, dim3(1), dim3(1), 0, s, set[0].count, (uint32_t)p);
+    hipLaunchKernelGGL((seed_set_kernel<C, HID>), dim3((unsigned)((p / 2 + 63) / 64)), dim3(64), 0, s, state, theta,
+                       p, seed, sigma, set[0], cap);
+    status = launch_status();
+    cur = 0;
+  }
+  for (; status == HIPENVS_OK && done < horizon; done += len, len = chunk_steps) {
     status = launch_later_chunk<C, HID>(state, theta, p, set[cur], set[1 - cur], cap, grid, gb, len, horizon, iters,
                                         alive, fall, gate, af, ad, fitness, steps, s);
     cur = 1 - cur;

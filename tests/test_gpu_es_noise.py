@@ -78,10 +78,13 @@ def test_cartpole_and_acrobot_seeded_rollouts(dev, p, hidden):
         assert expect.max().item() > 0
 
 
-@pytest.mark.parametrize("c,hidden,p", [(4, 64, 640), (4, 16, 20_000), (3, 64, 3000), (2, 32, 3000), (1, 8, 130)])
+@pytest.mark.parametrize("c,hidden,p", [(4, 64, 640), (4, 16, 20_000), (3, 64, 3000), (3, 32, 5_002),
+                                         (2, 32, 3000), (2, 16, 16_446), (1, 8, 130), (1, 8, 8_322)])
 def test_legged_seeded_rollout(dev, c, hidden, p):
-    """Populations the group tail takes whole (640, 130, 3000 at or below 16 per CU) and one
-    that runs compacted chunks first (20,000), with and without the assist spring."""
+    """Populations the group tail takes whole (640, 130, 3000: at most 16 members per CU at
+    C >= 3, 32 at C <= 2) and ones that run a first chunk over antithetic pairs and then
+    compacted chunks (20,000, 5,002, 16,446, 8,322; the last pair tile of each partly
+    filled), with and without the assist spring."""
     from hipenvs import es_noise, legged, legged_rollout
 
     d = legged_rollout.n_params(hidden, c)
