@@ -145,10 +145,11 @@ def test_bad_populations_are_rejected(dev):
     assert l.hipenvs_cartpole_es_rollout_seeded(null, null, 4, 0, 0.1, 32, 10, null, null, 0, null) == _lib.E_ARG
 
 
-@pytest.mark.parametrize("c,iters", [(4, 4), (4, 8), (4, 16), (2, 4), (2, 8), (2, 16)])
+@pytest.mark.parametrize("c,iters", [(4, 4), (4, 8), (4, 16), (2, 4), (2, 8), (2, 16), (3, 8), (1, 8)])
 def test_config4_full_size_schedules_agree(dev, c, iters):
     """At the benchmark's full shape (N = 262,144, H = 64, horizon 1,000, sigma 0.03 around
-    0.1 N(0, 1)) for the quadruped and the biped at S = 4, 8, 16: the seeded rollout, the
+    0.1 N(0, 1)) for the quadruped and the biped at S = 4, 8, 16, and for three legs and one
+    at S = 8: the seeded rollout, the
     chunked rollout of the perturbed columns, the chunked rollout of the perturbed rows (the
     drop-in call) and the one-member-per-lane rollout of the rows agree member for member."""
     from hipenvs import es_noise, legged, legged_rollout
@@ -168,4 +169,6 @@ def test_config4_full_size_schedules_agree(dev, c, iters):
     assert torch.equal(fs, fc) and torch.equal(ss, sc)
     assert torch.equal(fs, fr) and torch.equal(ss, sr)
     assert torch.equal(fs, fd) and torch.equal(ss, sd)
-    assert sr.max().item() == 1000 or sr.max().item() > 300  # a long tail reaches the group phase
+    # the benchmark's bodies have a long tail that reaches the group phase; every body
+    # outlives the first chunk
+    assert sr.max().item() > (300 if c in (2, 4) else 32)
