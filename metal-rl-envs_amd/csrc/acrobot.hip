@@ -223,29 +223,29 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
                                                            const float* __restrict__ theta, int64_t member_stride,
                                                            int64_t p, int32_t horizon, float out_sign,
                                                            float* __restrict__ steps_out) {
-  constexpr int D = 10 * H + 3, G = kRolloutLanes, U = (H + G - 1) / G;
-  __shared__ float xh_all[kRolloutMembers * H];
+  constexpr int G = kRolloutLanes, U = (H + G - 1) / G;
+  __shared__ float xp_all[kRolloutMembers * 3 * H];
   __shared__ float xl_all[kRolloutMembers * 4];
   const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
-  float* xh = xh_all + mloc * H;
+  float* xp = xp_all + mloc * 3 * H;  // head o's terms h_j * w2[j][o] at o * H + j
   float* xl = xl_all + mloc * 4;
   const int64_t i = (int64_t)blockIdx.x * kRolloutMembers + mloc;
   bool alive = i < p;
   const int64_t m = alive ? i : p - 1;  // a group past p steps member p - 1, unused
   const float* row = theta + m * member_stride;
-  float w1[U][6], b1[U];
+  float w1[U][6], b1[U], w2[U][3];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int j = g + G * u < H ? g + G * u : 0;  // lanes past H recompute unit 0, unused
 #pragma unroll
     for (int k = 0; k < 6; ++k) w1[u][k] = row[k * H + j];
     b1[u] = row[6 * H + j];
+#pragma unroll
+    for (int oo = 0; oo < 3; ++oo) w2[u][oo] = row[7 * H + 3 * j + oo];
   }
   const int o = g < 3 ? g : 0;
-  float w2[H];
-#pragma unroll
-  for (int j = 0; j < H; ++j) w2[j] = row[7 * H + 3 * j + o];
   const float b2 = row[10 * H + o];
+  const float* xo = xp + o * H;
   S4 s{state[m], state[p + m], state[2 * p + m], state[3 * p + m]};
   float steps = 0.0f;
   int32_t t = 0;
@@ -259,19 +259,25 @@ __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restri
     ob[3] = tr.sin_b;
     ob[4] = s.c;
     ob[5] = s.d;
+    // each lane forms its units' head terms h_j * w2[j][o], and lanes 0-2 add them in
+    // order: the same products and sums as one lane summing l + h_j * w2[j][o], with the
+    // multiplications spread over the group instead of repeated on the head lanes
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float pre = ob[0] * w1[u][0];
 #pragma unroll
       for (int k = 1; k < 6; ++k) pre = pre + ob[k] * w1[u][k];
       const float h = det_tanh(pre + b1[u]);
-      if (g + G * u < H) xh[g + G * u] = h;
+      if (g + G * u < H) {
+#pragma unroll
+        for (int oo = 0; oo < 3; ++oo) xp[oo * H + g + G * u] = h * w2[u][oo];
+      }
     }
     __syncthreads();
     if (g < 3) {
       float l = b2;
 #pragma unroll
-      for (int j = 0; j < H; ++j) l = l + xh[j] * w2[j];
+      for (int j = 0; j < H; ++j) l = l + xo[j];
       xl[g] = l;
     }
     __syncthreads();

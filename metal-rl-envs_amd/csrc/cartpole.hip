@@ -181,45 +181,51 @@ template <int H>
 __global__ __launch_bounds__(64) void rollout_group_kernel(const float* __restrict__ state,
                                                            const float* __restrict__ theta, int64_t member_stride,
                                                            int64_t p, int32_t horizon, float* __restrict__ fitness) {
-  constexpr int D = 7 * H + 2, G = kRolloutLanes, U = (H + G - 1) / G;
-  __shared__ float xh_all[kRolloutMembers * H];
+  constexpr int G = kRolloutLanes, U = (H + G - 1) / G;
+  __shared__ float xp_all[kRolloutMembers * 2 * H];
   __shared__ float xl_all[kRolloutMembers * 2];
   const int g = (int)threadIdx.x % G, mloc = (int)threadIdx.x / G;
-  float* xh = xh_all + mloc * H;
+  float* xp = xp_all + mloc * 2 * H;  // head o's terms h_j * w2[j][o] at o * H + j
   float* xl = xl_all + mloc * 2;
   const int64_t i = (int64_t)blockIdx.x * kRolloutMembers + mloc;
   bool alive = i < p;
   const int64_t m = alive ? i : p - 1;  // a group past p steps member p - 1, unused
   const float* row = theta + m * member_stride;
-  float w1[U][4], b1[U];
+  float w1[U][4], b1[U], w2[U][2];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int j = g + G * u < H ? g + G * u : 0;  // lanes past H recompute unit 0, unused
 #pragma unroll
     for (int k = 0; k < 4; ++k) w1[u][k] = row[k * H + j];
     b1[u] = row[4 * H + j];
+    w2[u][0] = row[5 * H + 2 * j];
+    w2[u][1] = row[5 * H + 2 * j + 1];
   }
   const int o = g < 2 ? g : 0;
-  float w2[H];
-#pragma unroll
-  for (int j = 0; j < H; ++j) w2[j] = row[5 * H + 2 * j + o];
   const float b2 = row[7 * H + o];
+  const float* xo = xp + o * H;
   float x = state[m], xd = state[p + m], th = state[2 * p + m], thd = state[3 * p + m];
   float survived = 0.0f;
   int32_t t = 0;
   alive = alive && horizon > 0;
   while (__any(alive)) {  // every lane steps, so the barriers stay uniform
+    // each lane forms its units' head terms h_j * w2[j][o], and lanes 0 and 1 add them in
+    // order: the same products and sums as one lane summing l + h_j * w2[j][o], with the
+    // multiplications spread over the group instead of repeated on the head lanes
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float pre = (((x * w1[u][0] + xd * w1[u][1]) + th * w1[u][2]) + thd * w1[u][3]) + b1[u];
       const float h = det_tanh(pre);
-      if (g + G * u < H) xh[g + G * u] = h;
+      if (g + G * u < H) {
+        xp[g + G * u] = h * w2[u][0];
+        xp[H + g + G * u] = h * w2[u][1];
+      }
     }
     __syncthreads();
     if (g < 2) {
       float l = b2;
 #pragma unroll
-      for (int j = 0; j < H; ++j) l = l + xh[j] * w2[j];
+      for (int j = 0; j < H; ++j) l = l + xo[j];
       xl[g] = l;
     }
     __syncthreads();

@@ -100,6 +100,21 @@ def test_legged_seeded_rollout(dev, c, hidden, p):
     assert longest > 16  # members outlived the first chunk
 
 
+@pytest.mark.parametrize("horizon", [1, 10, 33])
+def test_legged_seeded_short_horizon(dev, horizon):
+    """Horizons inside and just past the first chunk (32 steps at C = 4) on the pairs path."""
+    from hipenvs import es_noise, legged, legged_rollout
+
+    c, hidden, p = 4, 16, 20_002
+    d = legged_rollout.n_params(hidden, c)
+    theta = torch.from_numpy(theta0(d, 77)).to(dev)
+    state = legged.Legged(c).reset(p, seed=8, device=dev)
+    fs, ss = legged_rollout.rollout_seeded(state, theta, 5, 0.03, hidden, horizon, c)
+    fr, sr = legged_rollout.rollout(state, es_noise.perturb(theta, p, 5, 0.03), hidden, horizon, c, schedule="rows")
+    assert torch.equal(fs, fr) and torch.equal(ss, sr), horizon
+    assert sr.max().item() == horizon
+
+
 def test_legged_seeded_zero_horizon(dev):
     from hipenvs import legged, legged_rollout
 
