@@ -96,11 +96,11 @@ CARTPOLE_BYTES = 41
 # 0.0001 --copy-mib 256`, `bench.py --only aba --skip-cpu --copy-mib 256` (`--only steps` for the
 # step bodies) and `bench.py --only legged --skip-cpu --repeats 1 --copy-mib 256`, in KiB per
 # dispatch. The same counters read
-# 131085.3 and 262144.0 KiB for the 256 MiB device copy in the same process, so FETCH_SIZE is
+# 131085.3-131085.4 and 262144.0 KiB for the 256 MiB device copy in the same process, so FETCH_SIZE is
 # scaled by 2.000 and WRITE_SIZE by 1.000. Algorithmic bytes: 41 x N for the CartPole step.
 # Tables and commands: profiles/cartpole_step_n262144.md, profiles/aba_euler_n65536.md,
 # profiles/legged_es_rollout_n262144.md, profiles/step_bodies_and_evaluate.md.
-CARTPOLE_TRAFFIC = {1 << 18: 10793055, 1 << 20: 43192478, 1 << 24: 689698805}
+CARTPOLE_TRAFFIC = {1 << 18: 10793034, 1 << 20: 43187100, 1 << 24: 689700249}
 ABA_TRAFFIC = {4: 4649746, 16: 17437438, 64: 99818014}
 ABA_RK4_TRAFFIC = {4: 5102694, 16: 18511667, 32: 37387878, 64: 405806592}  # profiles/aba_rk4_n65536.md
 # The reference's articulated-body kernel (RK4, eval every 32) at N = 65,536 on its M3 Pro,
@@ -344,14 +344,16 @@ def module_api_rate(n, steps, dev):
 
 
 # Average duration of cp::step_kernel per dispatch in the rocprofv3 kernel trace of the
-# default command (`bench.py`, all of whose step launches at a given N are traced), in ns;
+# default command's CartPole block (`bench.py --only cartpole --skip-cpu`: the headline loop,
+# the step alone, 2^20 and 2^24, all of whose step launches at a given N are traced; the
+# default run's bounded sweep would add its short graphs), in ns;
 # profiles/cartpole_step_n262144.md tabulates them. The tracer runs each dispatch on its own,
 # so these include the per-dispatch ramp and drain that back-to-back launches overlap.
-CARTPOLE_TRACE_NS = {1 << 18: 3561.5, 1 << 20: 8518.8, 1 << 24: 110860.0}
+CARTPOLE_TRACE_NS = {1 << 18: 3293.4, 1 << 20: 8341.3, 1 << 24: 110995.6}
 # sha256 (first 16 hex digits) of the sources the traced kernel was built from,
 # csrc/cartpole.hip then csrc/hipenvs_device.h: when the sources differ, the trace no longer
 # describes this build, and cartpole_roofline falls back to the run's own HIP-event figure.
-CARTPOLE_TRACE_SOURCE_SHA = "056ec841d737ef48"
+CARTPOLE_TRACE_SOURCE_SHA = "5bda771dbf5c067d"
 CARTPOLE_TRACE_SOURCES = ("metal-rl-envs_amd/csrc/cartpole.hip", "metal-rl-envs_amd/csrc/hipenvs_device.h")
 
 
