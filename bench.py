@@ -109,9 +109,10 @@ ABA_RK4_REFERENCE = {4: 450437382, 8: 184284347, 16: 68215640, 32: 17807725, 64:
 STEP_BODY_TRAFFIC = {"pendulum_k2": 2833253, "pendulum_k4": 5104345, "pendulum_k8": 9586116,
                      "pendulum_k16": 19185779, "hopper": 4889324, "acrobot": 10906005, "legged4_s8": 8227360,
                      "legged4_s8_reference": 16402468}
-# per rollout (every chunk, group-chunk and tail kernel of one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 103070300949, (4, 8): 116239504630, (4, 16): 125435736933,
-                          (2, 4): 45783718429, (2, 8): 48714675453, (2, 16): 65271232788}
+# per rollout of the drop-in call on (P, D) rows (every chunk, group-chunk and tail kernel of
+# one rollout), keyed by (C, S)
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 89154403897, (4, 8): 101961901038, (4, 16): 110606830110,
+                          (2, 4): 44086167912, (2, 8): 46748505331, (2, 16): 62883762100}
 
 
 def log(msg):
@@ -540,16 +541,19 @@ def legged_population(dev, p, c, hidden, sigma=0.03, seed=0):
 
 def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats, alive_at=()):
     """(median wall s, median HIP-event s, steps taken, mean fitness) of full rollouts, and
-    with alive_at the members still alive after each of those step counts."""
+    with alive_at the members still alive after each of those step counts. schedule
+    "dropin" is the drop-in call: the chunked schedule on the caller's (P, D) rows;
+    "chunked" the same schedule on (D, P) columns; "rows"/"columns" one member per lane."""
     import torch
 
     from hipenvs import legged_rollout
 
     cols = schedule in ("columns", "chunked")
     small = theta[:, :64].contiguous() if cols else theta[:64].contiguous()
+    sched = "chunked" if schedule == "dropin" else schedule
     kw = {"theta_cols": small} if schedule == "chunked" else {}
     legged_rollout.rollout(state[:, :64].contiguous(), None if kw else small, hidden, 4, c, iters=sweeps,
-                           schedule=schedule, **kw)
+                           schedule=sched, **kw)
     torch.cuda.synchronize()
     walls, evs, taken, fit = [], [], None, None
     for _ in range(repeats):
@@ -559,7 +563,7 @@ def time_rollout(state, theta, hidden, horizon, c, sweeps, schedule, repeats, al
         start.record()
         kw = {"theta_cols": theta} if schedule == "chunked" else {}
         fit, steps = legged_rollout.rollout(state, None if kw else theta, hidden, horizon, c, iters=sweeps,
-                                            schedule=schedule, **kw)
+                                            schedule=sched, **kw)
         end.record()
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
@@ -589,9 +593,10 @@ def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
     d = legged_rollout.n_params(hidden, c)
     first = ", the first 16" if c <= 2 else ""
     out = {"n_envs": p, "c": c, "hidden": hidden, "horizon": horizon, "sigma": 0.03, "alive_bonus": 1.0,
-           "schedule": f"chunked ({legged_rollout.CHUNK_STEPS} steps{first}), columns layout", "by_sweeps": {}}
+           "schedule": f"chunked ({legged_rollout.CHUNK_STEPS} steps{first}), the drop-in call on the caller's "
+                       f"(P, D) rows", "by_sweeps": {}}
     for s in sweeps_list:
-        wall, ev, taken, fit_mean, alive = time_rollout(state, theta_cols, hidden, horizon, c, s, "chunked",
+        wall, ev, taken, fit_mean, alive = time_rollout(state, theta, hidden, horizon, c, s, "dropin",
                                                         args.repeats, alive_at=ALIVE_AT)
         flops = legged_flops_per_step(c, s, hidden)
         achieved_tf = taken * flops / ev / 1e12
@@ -612,32 +617,18 @@ def bench_legged(args, dev, c=4, sweeps_list=(4, 8, 16)):
             "alive_after_steps": {str(t): n for t, n in alive.items()},
         }
         out["by_sweeps"][str(s)] = rec
-        log(f"legged{c} ES rollout N={p} H={hidden} S={s} (chunked): {rec['env_steps_per_s']:,.0f} env-steps/s "
+        log(f"legged{c} ES rollout N={p} H={hidden} S={s} (drop-in rows): {rec['env_steps_per_s']:,.0f} env-steps/s "
             f"(mean episode {taken / p:.1f} steps, {ev * 1e3:.1f} ms), {achieved_tf:.2f} TFLOP/s algorithmic, "
             f"weights read at {rec['weight_stream_gbs']:.0f} GB/s")
         log(f"  alive after t steps: {', '.join(f'{t}: {n:,}' for t, n in alive.items() if t in ALIVE_AT)}; "
             f"member-steps in the first 32 steps: {alive['steps_in_first_32']:,}")
-    # the drop-in call with the reference's (P, D) rows, which the first chunk reads directly
-    # (each lane its member's row) instead of the (D, P) columns above
-    walls, evs = [], []
-    for _ in range(args.repeats):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record()
-        fit, steps = legged_rollout.rollout(state, theta, hidden, horizon, c, iters=8)
-        end.record()
-        torch.cuda.synchronize()
-        walls.append(time.perf_counter() - t0)
-        evs.append(start.elapsed_time(end) / 1e3)
-    taken = float(steps.double().sum().item())
-    cols_rec = out["by_sweeps"].get("8")
-    out["drop_in_rows_s8"] = {"env_steps_per_s": taken / statistics.median(walls), "wall_s": statistics.median(walls),
-                              "kernel_event_s": statistics.median(evs),
-                              "same_steps_as_columns": cols_rec is None or taken == cols_rec["steps_taken"]}
-    log(f"legged{c} drop-in rows call, S=8: {taken / statistics.median(walls):,.0f} env-steps/s, "
-        f"{statistics.median(evs) * 1e3:.1f} ms")
-    del fit, steps
+    # the same schedule on pre-transposed (D, P) columns, whose first chunk reads weight d of
+    # 64 members as one 256-byte row
+    wall, ev, taken, _ = time_rollout(state, theta_cols, hidden, horizon, c, 8, "chunked", args.repeats)
+    rows_rec = out["by_sweeps"].get("8")
+    out["columns_s8"] = {"env_steps_per_s": taken / wall, "wall_s": wall, "kernel_event_s": ev,
+                         "same_steps_as_rows": rows_rec is None or taken == rows_rec["steps_taken"]}
+    log(f"legged{c} chunked rollout on (D, P) columns, S=8: {taken / wall:,.0f} env-steps/s, {ev * 1e3:.1f} ms")
     if c == 4:
         wall, ev, taken, _ = time_rollout(state, theta, hidden, horizon, c, 8, "rows", 1)
         out["static_rows_s8_env_steps_per_s"] = taken / wall
@@ -1216,7 +1207,8 @@ def main():
         value, wall = rec["env_steps_per_s"], rec["wall_s"]
         roofline = rec["roofline"]
         cpu = extra["legged4_es_rollout"].get("cpu_baseline")
-        config = {"workload": f"legged4 ES rollout, N={args.legged_n}, H=64, S=8, horizon {args.legged_horizon}",
+        config = {"workload": f"legged4 ES rollout (the drop-in call on (P, D) rows), N={args.legged_n}, H=64, S=8, "
+                              f"horizon {args.legged_horizon}",
                   "n_envs": args.legged_n}
         ms = wall * 1e3
         steps = args.legged_horizon
