@@ -1,28 +1,17 @@
 """The mass-matrix K-link pendulum oracle (oracle/pendulum.py, the oracle of the HIP
-pendulum_metal step) pinned by the reference's test_pendulum.py (CPU): the textbook
-double pendulum, energy conservation, resets in place; and numpy's reduction order,
-which the kernel reproduces, made explicit."""
-
-import math
+pendulum_metal step) pinned by the reference's test_pendulum.py (CPU): a chain of point
+masses by the Jacobian method (the textbook double pendulum at K = 2), energy
+conservation, resets in place; and numpy's reduction order, which the kernel
+reproduces, made explicit."""
 
 import numpy as np
 import pytest
 
+import point_mass_chain
 from oracle import detmath
 from oracle import pendulum as op
 
 F32 = np.float32
-
-
-def double_pendulum_scalar(th1, th2, om1, om2, torque):
-    """test_pendulum.py:14-24: unit masses and rods, absolute angles, Cramer's rule."""
-    g = 9.8
-    m11, m22 = 2.0, 1.0
-    m12 = math.cos(th1 - th2)
-    b1 = torque - math.sin(th1 - th2) * om2**2 - 2 * g * math.sin(th1)
-    b2 = math.sin(th1 - th2) * om1**2 - g * math.sin(th2)
-    det = m11 * m22 - m12 * m12
-    return (b1 * m22 - m12 * b2) / det, (m11 * b2 - m12 * b1) / det
 
 
 def random_state(k, n, seed=0, vel=1.0):
@@ -32,13 +21,18 @@ def random_state(k, n, seed=0, vel=1.0):
 
 
 @pytest.mark.parametrize("trig", ["numpy", "det"])
-def test_k2_matches_double_pendulum(trig):
-    """test_pendulum.py:32-38."""
-    state, action = random_state(2, 100)
+@pytest.mark.parametrize("k,bound", [(2, 3e-6), (3, 6e-6), (4, 1e-5), (8, 3e-5), (16, 1e-4)])
+def test_matches_point_mass_chain(trig, k, bound):
+    """test_pendulum.py:32-38's textbook double pendulum (rtol 1e-3) at every K: the float32
+    mass-matrix step's accelerations against the chain's by the Jacobian method in float64
+    (tests/point_mass_chain.py), relative to |a| + 1. Measured: 1.4e-6 at K = 2, 4.3e-6 at
+    4, 1.5e-5 at 8, 4.3e-5 at 16."""
+    state, action = random_state(k, 100, seed=k)
     torque = ((action - 1) * op.TORQUE).astype(F32)
-    acc = op.mass_matrix_dsdt(state, torque, 2, trig=trig)[2:]
-    expect = np.array([double_pendulum_scalar(*s, t) for s, t in zip(state.T.tolist(), torque)]).T
-    np.testing.assert_allclose(acc, expect, rtol=1e-3, atol=1e-3)
+    acc = op.mass_matrix_dsdt(state, torque, k, trig=trig)[k:]
+    expect = point_mass_chain.batch_accelerations(state[:k].astype(np.float64), state[k:].astype(np.float64),
+                                                  torque.astype(np.float64))
+    assert (np.abs(acc - expect) / (np.abs(expect) + 1.0)).max() < bound
 
 
 def test_energy_is_conserved_without_torque():
