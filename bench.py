@@ -345,12 +345,11 @@ def module_api_rate(n, steps, dev):
 
 
 # Average duration of cp::step_kernel per dispatch in the rocprofv3 kernel trace of the
-# default command's CartPole block (`bench.py --only cartpole --skip-cpu`: the headline loop,
-# the step alone, 2^20 and 2^24, all of whose step launches at a given N are traced; the
-# default run's bounded sweep would add its short graphs), in ns;
+# default command (`bench.py`, all of whose step launches at a given N are traced: the
+# headline loop, the step alone and the bounded sweep's graphs), in ns;
 # profiles/cartpole_step_n262144.md tabulates them. The tracer runs each dispatch on its own,
 # so these include the per-dispatch ramp and drain that back-to-back launches overlap.
-CARTPOLE_TRACE_NS = {1 << 18: 3293.4, 1 << 20: 8341.3, 1 << 24: 110995.6}
+CARTPOLE_TRACE_NS = {1 << 18: 3433.3, 1 << 20: 8353.0, 1 << 24: 110188.9}
 # sha256 (first 16 hex digits) of the sources the traced kernel was built from,
 # csrc/cartpole.hip then csrc/hipenvs_device.h: when the sources differ, the trace no longer
 # describes this build, and cartpole_roofline falls back to the run's own HIP-event figure.
