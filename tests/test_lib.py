@@ -58,6 +58,29 @@ def test_bad_arguments_are_rejected_before_any_launch():
     assert l.hipenvs_sample_actions(null, 8, 257, 0, null) == _lib.E_ARG
 
 
+def test_legged_rollout_entry_points_check_their_shapes_on_the_host():
+    """The chunked rollouts return before any launch for a misaligned rows pointer, a rows
+    array past the 32-bit byte offsets, a short workspace, an odd or tiny seeded population
+    and an unsupported leg count. The addresses are never dereferenced."""
+    from hipenvs import _lib
+
+    l = _lib.lib()
+    p_ = ctypes.c_void_p
+    ok, odd = p_(1 << 20), p_((1 << 20) + 2)
+    args = (1.0, 0.0, 0.0, 0.0, ok, ok)
+    need = l.hipenvs_legged_es_rollout_workspace_bytes(4, 64, 4096)
+    rows = l.hipenvs_legged_es_rollout_chunked_rows
+    assert rows(4, 64, 8, 32, ok, odd, 4096, 10, *args, ok, need, None) == _lib.E_ARG
+    assert rows(4, 64, 8, 32, ok, ok, 4096, 10, *args, ok, need - 1, None) == _lib.E_ARG
+    big = (1 << 31) // (1676 * 4) + 1  # p * D * 4 >= 2^31 at C = 4, H = 64
+    assert rows(4, 64, 8, 32, ok, ok, big, 10, *args, ok, 1 << 62, None) == _lib.E_UNSUPPORTED
+    assert rows(5, 64, 8, 32, ok, ok, 4096, 10, *args, ok, 1 << 62, None) == _lib.E_UNSUPPORTED
+    seeded = l.hipenvs_legged_es_rollout_seeded
+    assert seeded(4, 64, 8, 32, ok, ok, 4097, 1, 0.03, 10, *args, ok, 1 << 62, None) == _lib.E_ARG
+    assert seeded(4, 64, 8, 32, ok, ok, 1, 1, 0.03, 10, *args, ok, 1 << 62, None) == _lib.E_ARG
+    assert seeded(4, 64, 8, 32, ok, ok, 4096, 1, 0.03, 10, *args, ok, need - 1, None) == _lib.E_ARG
+
+
 def test_python_wrappers_check_tensors():
     import torch
 
