@@ -397,7 +397,9 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
     // does after it: (den > 0) ? max0(q) : 0, that is 0 where den > 0 fails or q < 0, else q
     // (-0 and NaN pass, as in max0). Lanes 0 and 1 compare against -inf, which nothing is
     // below, and pass their stick quotients on unchanged. One clamp on two lanes replaces two
-    // on every lane.
+    // on every lane. No mask on the chain from the quotients to the impulses is combined on
+    // the scalar unit, which would wait for the vector compare to complete: the gate's mask
+    // is formed before the quotients, and the clamp and the gate are each one compare.
     const bool edge = (g == 2 || g == 3);
     const float qlo = edge ? 0.0f : -__builtin_inff();
     float cA[C][C], cB[C][C], w0x[C], qP[C], qQ[C], qd[C], slipc[C];
@@ -421,8 +423,18 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
       qd[k] = xc[sel];
       qr[k] = *reinterpret_cast<const double*>(xc + 4 + 2 * sel);
       qzero[k] = edge && !(qd[k] > 0.0f);  // lane 2 holds den_p, lane 3 den_m
+      // such a lane divides -1 by 1 instead, whose quotient the clamp sets to 0: the clamp
+      // then needs no mask of its own (a mask combined on the scalar unit between the
+      // quotient and its broadcast waits for the vector compare)
+      qd[k] = qzero[k] ? 1.0f : qd[k];
+      qr[k] = qzero[k] ? 1.0 : qr[k];
       slipc[k] = blk[k].Att * MU + blk[k].Atn;
     }
+    // -1 in a register the compiler cannot see through: an impulse whose contact is not
+    // pushing (open below) is gated as max(-1, ...) would be, by one compare of a select
+    // rather than two compares combined on the scalar unit
+    float neg_one = -1.0f;
+    asm volatile("" : "+v"(neg_one));
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
       for (int k = 0; k < C; ++k) {
@@ -447,9 +459,10 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         const bool touching = depth[k] >= 0.0f;
         const float target = BAUMGARTE_OVER_H * max0(depth[k]);
         const float tw = target - wn;
-        const float num = edge ? tw : qP[k] * wt + qQ[k] * tw;
+        const bool open = touching && (wn < target);  // known before the quotients
+        const float num = qzero[k] ? -1.0f : edge ? tw : qP[k] * wt + qQ[k] * tw;
         const float quo = div(num, qd[k], qr[k]);
-        const float qc = (qzero[k] || quo < qlo) ? 0.0f : quo;
+        const float qc = (quo < qlo) ? 0.0f : quo;
         const float ln_stick = lane_bcast<kGroup, 0>(qc);
         const float lt_stick = lane_bcast<kGroup, 1>(qc);
         const float ln_p = lane_bcast<kGroup, 2>(qc);
@@ -461,7 +474,7 @@ __device__ __forceinline__ void substep(float (&q)[3 + C], float (&v)[3 + C], co
         const float lt_slide = (MU * sgn) * ln_slide;
         const float lnv = sticks ? ln_stick : ln_slide;
         const float ltv = sticks ? lt_stick : lt_slide;
-        const bool active = touching && (lnv > 0.0f) && (wn < target);
+        const bool active = (open ? lnv : neg_one) > 0.0f;  // open && lnv > 0
         lt[k] = active ? ltv : 0.0f;
         ln[k] = active ? lnv : 0.0f;
       }
