@@ -111,8 +111,8 @@ STEP_BODY_TRAFFIC = {"pendulum_k2": 2833253, "pendulum_k4": 5104345, "pendulum_k
                      "legged4_s8_reference": 16402468}
 # per rollout of the drop-in call on (P, D) rows (every chunk, group-chunk and tail kernel of
 # one rollout), keyed by (C, S)
-LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 89154403897, (4, 8): 101961901038, (4, 16): 110606830110,
-                          (2, 4): 44086167912, (2, 8): 46748505331, (2, 16): 62883762100}
+LEGGED_ROLLOUT_TRAFFIC = {(4, 4): 89099891712, (4, 8): 101928242176, (4, 16): 110521539584,
+                          (2, 4): 44110212710, (2, 8): 46772397466, (2, 16): 62815717376}
 
 
 def log(msg):
